@@ -1,0 +1,315 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A8 linear path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Workload (the decode sweep): the four Qwen3-1.7B linear shapes as vLLM
+runs them (qkv 2048->4096, o_proj 2048->2048, gate_up 2048->12288, down 6144->2048) at
+M in {1,2,4,8,16,17,32,64,128}, bias off and on: 72 W8A8 linears.  One step replays all
+72 as one HIP graph.  Operands are the benchmark's seeded synthetic data (x ~ N(0,1),
+W ~ N(0,0.02), bias ~ N(0,0.01), bf16, quantized per token / per channel), already in HBM.
+Weights rotate through enough distinct copies (>= 512 MiB) that no call finds its weights
+in the 256 MiB Infinity Cache.  `value` is the mean microseconds per linear over the sweep.
+
+After the timed steps (not inside them): per-call graph-replay times of every sweep point,
+the roofline object of the dominant kernel (HIP events on the launch stream, algorithmic
+bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3), and the
+CPU baseline (the oracle's CPU restatement of the reference's path, on a bounded sample).
+Every GPU output is checked against a float64 reference before it is timed, after the
+output buffer has been poisoned.  Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "int8-linear_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
+DECODE_M = [1, 2, 4, 8, 16, 17, 32, 64, 128]
+PREFILL_M = [512, 1024, 2048, 4096]
+QUANT_M = [1, 16, 128, 1024, 4096]
+ROTATE_BYTES = 768 << 20
+METRIC = "W8A8 linear µs & % of HBM/int8 roofline, M=1-4096; µs per decoder-layer stand-in"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemm_bytes(m: int, k: int, n: int, bias: bool) -> int:
+    """Algorithmic HBM bytes of one W8A8 linear: int8 A and B, fp32 scales, bf16 out/bias."""
+    return m * k + k * n + 4 * m + 4 * n + 2 * m * n + (2 * n if bias else 0)
+
+
+def norm_bytes(m: int, h: int, residual: bool = True) -> int:
+    return (7 if residual else 3) * m * h + 2 * h + 4 * m
+
+
+def silu_bytes(m: int, i: int) -> int:
+    return 5 * m * i + 4 * m
+
+
+def graph_time_us(fn, calls: int, windows: int = 5) -> float:
+    """Median microseconds per call of `calls` back-to-back calls captured in one graph."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(calls):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(windows):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        g.replay()
+        e.record()
+        e.synchronize()
+        out.append(s.elapsed_time(e) * 1e3 / calls)
+    del g
+    return statistics.median(out)
+
+
+def check_linear(out, d) -> float:
+    """Max relative error against float64, relative to max(|ref|, |term|) (reference rule)."""
+    import torch
+    term = (d["a_q"].double() @ d["w_q"].double().t()) * d["a_s"].double() * d["w_s"].double().t()
+    ref = term + d["bias"].double() if d["bias"] is not None else term
+    scale = torch.maximum(ref.abs(), term.abs()).clamp_min(1e-6)
+    return ((out.double() - ref).abs() / scale).max().item()
+
+
+class Sweep:
+    """The decode sweep's operands, with weight copies rotated across calls."""
+
+    def __init__(self, shapes, ms, device):
+        import torch
+
+        from int8_linear.operands import operands, seed_of
+        self.points = []   # (label, m, k, n, bias, operand dict)
+        for label, k, n in shapes:
+            for m in ms:
+                for bias in (False, True):
+                    d = operands(m, k, n, seed_of(m, k, n), with_bias=bias, device=device)
+                    self.points.append((label, m, k, n, bias, d))
+        per_set = sum(k * n for _, k, n in shapes)
+        self.copies = max(2, -(-ROTATE_BYTES // per_set))
+        base = {(k, n): self.points[[p[2:4] for p in self.points].index((k, n))][5]["w_q"]
+                for _, k, n in shapes}
+        self.weights = {kn: [w] + [w.clone() for _ in range(self.copies - 1)]
+                        for kn, w in base.items()}
+        torch.cuda.synchronize()
+
+    def call(self, idx: int, copy: int):
+        from int8_linear import w8a8_mm
+        import torch
+        label, m, k, n, bias, d = self.points[idx]
+        w = self.weights[(k, n)][copy % self.copies]
+        return w8a8_mm(d["a_q"], w.t(), d["a_s"], d["w_s"], torch.bfloat16, d["bias"])
+
+
+def cpu_baseline() -> dict:
+    """The oracle's CPU restatement of the reference's path (exact int32 product + fp32
+    dequant + bf16 cast) on the config-0 shape, repeated for about 10 s."""
+    import numpy as np
+
+    from int8_linear.operands import operands, seed_of
+    from oracle import oracle as o
+    m, k, n = 16, 2048, 4096
+    d = operands(m, k, n, seed_of(m, k, n))
+    a, w = d["a_q"].numpy(), d["w_q"].numpy()
+    sa, sb = d["a_s"].numpy(), d["w_s"].numpy()
+    o.w8a8_mm(a, w, sa, sb)                     # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0 or reps < 5:
+        o.w8a8_mm(a, w, sa, sb)
+        reps += 1
+    us = (time.perf_counter() - t0) / reps * 1e6
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    return {"value": round(us, 2), "unit": "us per linear", "cores": threads,
+            "kind": "port",
+            "sample": f"config 0 (M=16, K=2048, N=4096, bf16 out), {reps} calls of the C oracle "
+                      f"(int32 GEMM + fp32 dequant), OpenMP threads={threads}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 2-3 and per-point table")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
+              "one MI355X); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from int8_linear import _lib
+    from int8_linear.shapes import SHAPES
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("library:", _lib.lib().i8l_version().decode(), "device:", torch.cuda.get_device_name())
+    shapes = SHAPES["qwen3-1.7b-vllm"]
+    sw = Sweep(shapes, DECODE_M, dev)
+    log(f"sweep: {len(sw.points)} linears, {sw.copies} weight copies")
+
+    # correctness first, into poisoned outputs
+    worst = 0.0
+    for i, (label, m, k, n, bias, d) in enumerate(sw.points):
+        torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
+        out = sw.call(i, 0)
+        err = check_linear(out, d)
+        worst = max(worst, err)
+        if not err <= 1e-2:
+            raise SystemExit(f"FAIL: {label} M={m} bias={bias}: max rel err {err}")
+    log(f"sweep checked against float64: worst rel err {worst:.3g}")
+
+    # one step = the whole sweep, each call on its own weight copy, one graph
+    def step_calls(rep: int):
+        for i in range(len(sw.points)):
+            sw.call(i, rep * len(sw.points) + i)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step_calls(0)
+    torch.cuda.current_stream().wait_stream(side)
+    graphs = []
+    for rep in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step_calls(rep)
+        graphs.append(g)
+    for i in range(args.warmup):
+        graphs[i % 2].replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        graphs[i % 2].replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    n_calls = len(sw.points)
+    us_per_linear = ms_per_step * 1e3 / n_calls
+    sweep_bytes = sum(gemm_bytes(m, k, n, b) for _, m, k, n, b, _ in sw.points)
+    log(f"step: {ms_per_step * 1e3:.1f} us for {n_calls} linears = {us_per_linear:.2f} us each; "
+        f"{sweep_bytes / (ms_per_step * 1e-3) / 1e9:.0f} GB/s")
+    del graphs
+
+    result = {
+        "metric": METRIC, "value": round(us_per_linear, 3), "unit": "us per linear (mean over decode sweep)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8xint8->int32, bf16 out", "data": "synthetic",
+        "config": {"workload": "BASELINE config 1: decode sweep, Qwen3-1.7B vLLM shapes "
+                               "(qkv 2048->4096, o 2048->2048, gate_up 2048->12288, "
+                               "down 6144->2048) x M{1,2,4,8,16,17,32,64,128} x bias{off,on}",
+                   "linears_per_step": n_calls, "weight_copies": sw.copies,
+                   "sweep_GBps": round(sweep_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
+    }
+
+    # roofline of the dominant kernel: the decode GEMM at config 0 (qkv, M=16), cold weights
+    qkv_idx = [i for i, p in enumerate(sw.points) if p[0] == "qkv_proj" and p[1] == 16 and not p[4]][0]
+    reps = 4 * sw.copies
+    us0 = graph_time_us(lambda i: sw.call(qkv_idx, i), reps)
+    b0 = gemm_bytes(16, 2048, 4096, False)
+    ach = b0 / (us0 * 1e-6) / 1e9
+    result["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                          "kernel": "gemm_stream (config 0: M=16 K=2048 N=4096)",
+                          "bytes_per_launch": b0, "avg_launch_us": round(us0, 3)}
+    log(f"roofline config0: {us0:.2f} us, {ach:.0f} GB/s ({ach / HBM_PEAK_GBS:.1%})")
+
+    if not args.no_extra:
+        table = []
+        for i, (label, m, k, n, bias, d) in enumerate(sw.points):
+            us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies, windows=3)
+            gbs = gemm_bytes(m, k, n, bias) / (us * 1e-6) / 1e9
+            table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
+        result["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
+        result["quant"] = bench_quant(dev)
+        result["prefill"] = bench_prefill(dev)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_quant(dev) -> dict:
+    """the two fused quantizers at H=2048 / I=6144."""
+    import torch
+
+    from int8_linear import fused_quant as fq
+    rows = []
+    for m in QUANT_M:
+        g = torch.Generator().manual_seed(m)
+        copies = max(2, -(-ROTATE_BYTES // (m * 2048 * 7 + 1)))
+        copies = min(copies, 64)
+        xs = [torch.randn((m, 2048), generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
+        rs = [torch.randn((m, 2048), generator=g).to(torch.bfloat16).to(dev) for _ in range(copies)]
+        w = (1 + 0.1 * torch.randn(2048, generator=g)).to(torch.bfloat16).to(dev)
+        us_n = graph_time_us(lambda i: fq.add_rmsnorm_quant(xs[i % 2], rs[i % copies], w, 1e-6), 2 * copies, 3)
+        copies_s = min(64, max(2, -(-ROTATE_BYTES // (m * 12288 * 2 + 1))))
+        gus = [torch.randn((m, 12288), generator=g).to(torch.bfloat16).to(dev) for _ in range(copies_s)]
+        us_s = graph_time_us(lambda i: fq.silu_mul_quant(gus[i % copies_s], True, True), 2 * copies_s, 3)
+        rows.append([m, round(us_n, 2), round(norm_bytes(m, 2048) / (us_n * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+                     round(us_s, 2), round(silu_bytes(m, 6144) / (us_s * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)])
+        del xs, rs, gus
+    return {"cols": ["M", "add_rmsnorm_quant_us", "hbm_frac", "silu_mul_quant_us", "hbm_frac"],
+            "rows": rows}
+
+
+def bench_prefill(dev) -> dict:
+    """Llama-3-8B shapes at prefill M; int8 TOP/s and MFMA fraction."""
+    import torch
+
+    from int8_linear import w8a8_mm
+    from int8_linear.operands import quant_rows
+    from int8_linear.shapes import SHAPES
+    rows = []
+    for label, k, n in SHAPES["llama-3-8b"]:
+        g = torch.Generator().manual_seed(k + n)
+        w = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16)
+        w_q, w_s = quant_rows(w)
+        w_q, w_s = w_q.to(dev), w_s.to(dev)
+        del w
+        for m in PREFILL_M:
+            x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+            a_q, a_s = quant_rows(x)
+            a_q, a_s = a_q.to(dev), a_s.to(dev)
+            out = w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16)
+            term = (a_q[:64].double() @ w_q.double().t()) * a_s[:64].double() * w_s.double().t()
+            err = ((out[:64].double() - term).abs() / term.abs().clamp_min(1e-6)).max().item()
+            if not err <= 1e-2:
+                raise SystemExit(f"FAIL prefill {label} M={m}: rel err {err}")
+            us = graph_time_us(lambda i: w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16), 10, 3)
+            tops = 2 * m * n * k / (us * 1e-6) / 1e12
+            rows.append([label, m, round(us, 2), round(tops, 1), round(tops / INT8_PEAK_TOPS, 3)])
+            log(f"prefill {label} M={m}: {us:.1f} us {tops:.0f} TOP/s")
+        del w_q, w_s
+    return {"cols": ["shape", "M", "us", "TOPs", "mfma_frac"], "rows": rows}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,145 @@
+/*
+ * int8_linear_amd.h -- C ABI of the MI355X (gfx950) W8A8 linear path.
+ *
+ * Every entry point takes raw device pointers, element strides, sizes, dtype codes and the
+ * caller's hipStream_t (passed as void* so that this header needs no HIP include).  The
+ * library never allocates, frees or synchronises, and never touches host memory on the hot
+ * path: it validates, launches on `stream`, and returns.  Launches are therefore legal
+ * inside hipGraph stream capture.  Outputs are allocated by the caller, as in the
+ * reference's Python wrappers (int8_linear/kernel.py:242, int8_linear/fused_quant.py:100-102,
+ * 118-119 of AshrithaG/int8-linear).
+ *
+ * Return value of every entry point is an i8l_status.  On a non-zero status,
+ * i8l_last_error() returns a thread-local, NUL-terminated description of the last failure.
+ * The Python host layer maps I8L_UNSUPPORTED to int8_linear.NotSupported, I8L_INVALID_ARG to
+ * ValueError and I8L_HIP_ERROR to RuntimeError, which is the reference's error convention
+ * (int8_linear/kernel.py:45-46, 221-238).
+ */
+#ifndef INT8_LINEAR_AMD_H
+#define INT8_LINEAR_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+  I8L_OK = 0,
+  I8L_UNSUPPORTED = 1, /* the kernels do not take this shape/dtype/config: caller falls back */
+  I8L_INVALID_ARG = 2, /* inconsistent shapes or sizes */
+  I8L_HIP_ERROR = 3    /* a HIP runtime call failed (launch error, no device, ...) */
+};
+
+/* Element type codes for bias, outputs and bf16/fp16 activations. */
+enum {
+  I8L_DTYPE_NONE = 0, /* "no tensor" (bias absent) */
+  I8L_BF16 = 1,
+  I8L_F16 = 2,
+  I8L_F32 = 3,
+  I8L_I32 = 4         /* GEMM output only: the raw int32 product (reference raw=True) */
+};
+
+/*
+ * Tile configuration of one GEMM launch; mirrors int8_linear.kernel.Config
+ * (reference int8_linear/kernel.py:49-60) with the MI355X meaning of each field:
+ *   bm, bn, bk : output rows (tokens) x output columns x K bytes per workgroup step
+ *   warps      : wavefronts (64 lanes) per workgroup
+ *   stages     : LDS buffers for the staged (prefill) schedule, 1 or 2
+ *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order)
+ *   split_k    : K-splits inside one workgroup (decode schedule), each wave sums one slice
+ * A config the library was not built for returns I8L_UNSUPPORTED.
+ */
+typedef struct i8l_config {
+  int32_t bm, bn, bk, warps, stages, group_m, split_k;
+} i8l_config;
+
+/*
+ * W8A8 scaled matmul:  out[m,n] = cast( f32(sum_k A[m,k]*B[k,n]) * sa[m|0] * sb[n|0] + f32(bias[n]) )
+ * with the int32 sum exact and the epilogue evaluated left to right in fp32 with no fused
+ * multiply-add, then one round-to-nearest-even cast.  out_dtype I8L_I32 writes the raw int32
+ * product and ignores scales and bias.
+ *
+ * A is int8 [M,K] at a + m*stride_am + k*stride_ak.  B is int8 [K,N] at b + k*stride_bk +
+ * n*stride_bn; the fast schedules want stride_bk == 1 (the transposed view of an [N,K]
+ * nn.Linear weight, as vLLM passes it).  Other strides and unaligned pointers run a
+ * correct generic kernel.  scale_a has scale_a_len 1 or M fp32 values, scale_b has 1 or N.
+ * bias is NULL (bias_dtype I8L_DTYPE_NONE) or N values of bf16/f16/f32.  out is [M,N] with
+ * row stride stride_cm and unit column stride, of out_dtype bf16/f16/f32/i32.
+ * cfg NULL picks the library default for (M,N,K).
+ *
+ * Replaces the reference's launch of the Triton kernel _w8a8_mm from
+ * w8a8_mm (int8_linear/kernel.py:202-257; kernel body 63-124).
+ */
+int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak,
+                const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                const float* scale_a, int64_t scale_a_len,
+                const float* scale_b, int64_t scale_b_len,
+                const void* bias, int32_t bias_dtype,
+                void* out, int64_t stride_cm, int32_t out_dtype,
+                int64_t M, int64_t N, int64_t K,
+                const i8l_config* cfg, void* stream);
+
+/*
+ * Whether i8l_w8a8_mm takes this (M,N,K,cfg) on a fast schedule: returns I8L_OK or
+ * I8L_UNSUPPORTED without launching anything (host-only; no GPU needed).  The decline
+ * rule is the reference's: N % bn or K % bk non-zero (int8_linear/kernel.py:228-229),
+ * or a tile the library was not built for.
+ */
+int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
+
+/* The default config the library uses for (M,N,K) (reference default_config,
+ * int8_linear/kernel.py:127-134, re-derived for MI355X). Host-only. */
+int i8l_default_config(int64_t M, int64_t N, int64_t K, i8l_config* cfg_out);
+
+/*
+ * Fused add + RMSNorm + per-token int8 quantize, one row per token:
+ *   x = f32(x) (+ f32(residual));  residual_out = cast(x)          (when residual != NULL)
+ *   var = sum(x^2)/H;  xn = x * rsqrt(var + eps)
+ *   y = cast_x( f32(cast_w(xn)) * f32(weight) )
+ *   scale = absmax(y)/127;  q = clamp(rne(y * 127/absmax), -128, 127)   (0 for a zero row)
+ * x, residual, residual_out: [M,H] contiguous of act_dtype (bf16/f16); weight [H] of
+ * w_dtype (bf16/f16); q int8 [M,H]; scale fp32 [M].  residual and residual_out are both
+ * NULL or both non-NULL.  precise_div 1 = IEEE divisions; 0 = multiply by the IEEE
+ * reciprocal.  M == 0 launches nothing.
+ * Replaces add_rmsnorm_quant / _add_rmsnorm_quant_kernel (int8_linear/fused_quant.py:56-73,
+ * 95-110); residual == NULL is rmsnorm_quant (fused_quant.py:132-135).
+ */
+int i8l_add_rmsnorm_quant(const void* x, const void* residual, const void* weight, float eps,
+                          int8_t* q, float* scale, void* residual_out,
+                          int64_t M, int64_t H, int32_t act_dtype, int32_t w_dtype,
+                          int32_t precise_div, void* stream);
+
+/*
+ * Fused SiLU-and-mul + per-token int8 quantize:
+ *   g = f32(gate_up[m, :I]), u = f32(gate_up[m, I:]);  a = g / (1 + exp(-g))
+ *   a = f32(cast(a)) if round_silu;  y = f32(cast(a*u));  then the quantizer above.
+ * gate_up [M, 2I] contiguous bf16/f16; q int8 [M,I]; scale fp32 [M].
+ * Replaces silu_mul_quant / _silu_mul_quant_kernel (int8_linear/fused_quant.py:76-88, 113-124).
+ */
+int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale,
+                       int64_t M, int64_t I, int32_t act_dtype,
+                       int32_t round_silu, int32_t precise_div, void* stream);
+
+/*
+ * Plain per-token int8 quantize of a bf16/f16 [M,H] contiguous tensor (the quantizer of
+ * int8_linear/fused_quant.py:41-53 on its own).  Stands in for vLLM's scaled_int8_quant,
+ * which the reference's decoder stand-in calls on the o_proj input
+ * (bench/fuse_quant.py:234, bench/situ_tune.py:110).
+ */
+int i8l_quant_per_token(const void* x, int8_t* q, float* scale,
+                        int64_t M, int64_t H, int32_t act_dtype,
+                        int32_t precise_div, void* stream);
+
+/* Thread-local description of the last failure ("" if none). */
+const char* i8l_last_error(void);
+
+/* Library version string, e.g. "int8_linear_amd 0.1.0 gfx950". */
+const char* i8l_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INT8_LINEAR_AMD_H */

@@ -1,0 +1,156 @@
+"""The activation quantizer fused into the kernel before it, as MI355X HIP kernels.
+
+A W8A8 layer quantizes its input per token right before the matmul.  These kernels fold
+that quantizer into the op that produces the input, one workgroup per token row:
+
+    add_rmsnorm_quant(x, residual, w, eps) -> (x_q, scale, residual_out)
+    rmsnorm_quant(x, w, eps)               -> (x_q, scale)
+    silu_mul_quant(gate_up)                -> (x_q, scale)
+    quant_per_token(x)                     -> (x_q, scale)
+
+Same Python surface and arithmetic as the reference's int8_linear/fused_quant.py
+(AshrithaG/int8-linear, 41-124): residual add and norm in fp32, the normalized value rounded
+to the weight dtype, times the weight, rounded to the activation dtype; SiLU optionally
+rounded before the multiply; then
+
+    scale = absmax / 127,   x_q = round_half_even(x * (127 / absmax)), saturated
+
+The sum of squares is a fixed pairwise tree in double, rsqrt is the correctly rounded
+double result rounded to float, and exp is a fixed Cody-Waite/Taylor routine, so the CPU
+oracle reproduces every code and scale bit for bit.  PRECISE_DIV=True selects IEEE
+division (the reference default); False multiplies by the IEEE reciprocal instead.
+
+Each is also a torch custom op, so torch.compile treats it as one opaque kernel.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from int8_linear import _lib
+from int8_linear.kernel import NotSupported
+
+_ACT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def _act_code(t: torch.Tensor, what: str) -> int:
+    code = _ACT.get(t.dtype)
+    if code is None:
+        raise NotSupported(f"{what} must be bfloat16 or float16, got {t.dtype}")
+    if not t.is_cuda:
+        raise NotSupported(f"{what} must be on a HIP device")
+    return code
+
+
+def add_rmsnorm_quant(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
+                      eps: float, precise_div: bool = True):
+    """(x_q int8 [M, K], scale fp32 [M, 1], residual_out [M, K] or None)."""
+    assert x.is_contiguous() and x.dim() == 2
+    M, K = x.shape
+    act = _act_code(x, "x")
+    wcode = _act_code(weight, "weight")
+    if weight.numel() != K:
+        raise ValueError(f"weight has {weight.numel()} values for rows of {K}")
+    weight = weight.contiguous()
+    if residual is not None:
+        assert residual.is_contiguous() and residual.shape == x.shape
+        if residual.dtype != x.dtype:
+            raise NotSupported("residual must have x's dtype")
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    rout = torch.empty_like(x) if residual is not None else None
+    if M:
+        status = _lib.lib().i8l_add_rmsnorm_quant(
+            x.data_ptr(), residual.data_ptr() if residual is not None else None,
+            weight.data_ptr(), float(eps), q.data_ptr(), s.data_ptr(),
+            rout.data_ptr() if rout is not None else None, M, K, act, wcode,
+            int(bool(precise_div)), _lib.stream_of(x))
+        _lib.check(status, NotSupported)
+    return q, s, rout
+
+
+def silu_mul_quant(gate_up: torch.Tensor, precise_div: bool = True, round_silu: bool = False):
+    """silu(gate) * up, quantized: (x_q int8 [M, I], scale fp32 [M, 1])."""
+    assert gate_up.is_contiguous() and gate_up.dim() == 2
+    M, I2 = gate_up.shape
+    I = I2 // 2
+    act = _act_code(gate_up, "gate_up")
+    q = torch.empty((M, I), dtype=torch.int8, device=gate_up.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=gate_up.device)
+    if M and I:
+        status = _lib.lib().i8l_silu_mul_quant(
+            gate_up.data_ptr(), q.data_ptr(), s.data_ptr(), M, I, act, int(bool(round_silu)),
+            int(bool(precise_div)), _lib.stream_of(gate_up))
+        _lib.check(status, NotSupported)
+    return q, s
+
+
+def quant_per_token(x: torch.Tensor, precise_div: bool = True):
+    """Per-token int8 quantization of a bf16/fp16 [M, K] tensor: (x_q, scale fp32 [M, 1]).
+
+    The quantizer of the two fused kernels on its own, with vLLM scaled_int8_quant's
+    convention; it quantizes the o_proj input, which has no kernel before it to fuse into.
+    """
+    assert x.is_contiguous() and x.dim() == 2
+    M, K = x.shape
+    act = _act_code(x, "x")
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    if M and K:
+        status = _lib.lib().i8l_quant_per_token(x.data_ptr(), q.data_ptr(), s.data_ptr(), M, K,
+                                                act, int(bool(precise_div)), _lib.stream_of(x))
+        _lib.check(status, NotSupported)
+    return q, s
+
+
+# Numerics the custom ops use (reference fused_quant.py:127-129 defaults);
+# vllm_fuse_patch.use_measured_numerics switches them to the served configuration.
+PRECISE_DIV = True
+ROUND_SILU = False
+
+
+@torch.library.custom_op("int8_linear::rmsnorm_quant", mutates_args=())
+def rmsnorm_quant_op(x: torch.Tensor, weight: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    q, s, _ = add_rmsnorm_quant(x.contiguous(), None, weight, eps, PRECISE_DIV)
+    return q, s
+
+
+@rmsnorm_quant_op.register_fake
+def _(x, weight, eps):
+    return (x.new_empty(x.shape, dtype=torch.int8),
+            x.new_empty((x.shape[0], 1), dtype=torch.float32))
+
+
+@torch.library.custom_op("int8_linear::add_rmsnorm_quant", mutates_args=())
+def add_rmsnorm_quant_op(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                         eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return add_rmsnorm_quant(x.contiguous(), residual.contiguous(), weight, eps, PRECISE_DIV)
+
+
+@add_rmsnorm_quant_op.register_fake
+def _(x, residual, weight, eps):
+    return (x.new_empty(x.shape, dtype=torch.int8),
+            x.new_empty((x.shape[0], 1), dtype=torch.float32),
+            torch.empty_like(x))
+
+
+@torch.library.custom_op("int8_linear::silu_mul_quant", mutates_args=())
+def silu_mul_quant_op(gate_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return silu_mul_quant(gate_up.contiguous(), PRECISE_DIV, ROUND_SILU)
+
+
+@silu_mul_quant_op.register_fake
+def _(gate_up):
+    return (gate_up.new_empty((gate_up.shape[0], gate_up.shape[1] // 2), dtype=torch.int8),
+            gate_up.new_empty((gate_up.shape[0], 1), dtype=torch.float32))
+
+
+@torch.library.custom_op("int8_linear::quant_per_token", mutates_args=())
+def quant_per_token_op(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return quant_per_token(x.contiguous(), PRECISE_DIV)
+
+
+@quant_per_token_op.register_fake
+def _(x):
+    return (x.new_empty(x.shape, dtype=torch.int8),
+            x.new_empty((x.shape[0], 1), dtype=torch.float32))

@@ -1,0 +1,173 @@
+"""W8A8 int8 matmul with the dequantization fused in, on MI355X (gfx950) HIP kernels.
+
+    C[M, N] = (A_q[M, K] @ W_q[K, N]) * scale_a[M] * scale_b[N] + bias[N]
+
+The same Python surface as the reference's int8_linear/kernel.py (AshrithaG/int8-linear):
+Config, NotSupported, default_config, tuned_config, choose_config and w8a8_mm, with the
+same argument meaning, validation order and exceptions (kernel.py:45-60, 127-160, 202-242).
+The kernel itself is hand-written HIP in csrc/i8l_gemm.hip, reached through the C ABI of
+include/int8_linear_amd.h: an int8 MFMA (v_mfma_i32_16x16x64_i8 / 32x32x32_i8) product
+accumulated exactly in int32, then acc * scale_a * scale_b + bias in fp32 and one cast.
+
+W_q is the transposed [K, N] view of an [N, K] nn.Linear weight (K-contiguous), which is
+how vLLM passes it.  Launches go on the caller's current stream and allocate nothing but
+the output, so calls can be captured into a HIP graph.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+from int8_linear import _lib
+
+TUNED_PATH = Path(__file__).with_name("tuned_configs.json")
+
+
+class NotSupported(Exception):
+    """The kernel does not take this shape or dtype, so the caller should fall back."""
+
+
+@dataclass(frozen=True)
+class Config:
+    """One GEMM launch configuration (reference kernel.py:49-60), in MI355X terms.
+
+    stages == 1 is the decode (weight-streaming) schedule: a workgroup of `warps` waves
+    covers bm tokens x bn columns and splits K across its waves, each taking 64-byte steps,
+    so bk == 64 * warps.  stages == 2 is the prefill schedule: a bm x bn macro tile staged
+    through double-buffered LDS, K in bk-byte steps, `warps` waves, `group_m` rows of tiles
+    walked together.  A configuration the library was not built with raises NotSupported.
+    """
+
+    bm: int
+    bn: int
+    bk: int
+    warps: int = 4
+    stages: int = 2
+    group_m: int = 1
+    split_k: int = 1
+
+    @property
+    def name(self) -> str:
+        base = f"{self.bm}x{self.bn}x{self.bk} w{self.warps} s{self.stages} g{self.group_m}"
+        return base if self.split_k == 1 else f"{base} k{self.split_k}"
+
+
+_cstructs: dict[Config, _lib.CConfig] = {}
+
+
+def _cconfig(cfg: Config) -> _lib.CConfig:
+    c = _cstructs.get(cfg)
+    if c is None:
+        c = _cstructs[cfg] = _lib.CConfig(cfg.bm, cfg.bn, cfg.bk, cfg.warps, cfg.stages,
+                                          cfg.group_m, cfg.split_k)
+    return c
+
+
+def default_config(m: int, n: int, k: int) -> Config:
+    """The untuned choice: the weight-streaming decode schedule up to 128 tokens, staged
+    macro tiles above (the library's own rule, i8l_default_config)."""
+    c = _lib.CConfig()
+    _lib.check(_lib.lib().i8l_default_config(m, n, k, c), NotSupported)
+    return Config(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, c.split_k)
+
+
+@lru_cache(maxsize=None)
+def _tuned_table(device_name: str) -> dict:
+    tables = json.loads(TUNED_PATH.read_text()) if TUNED_PATH.exists() else {}
+    return tables.get(device_name, {})
+
+
+def tuned_config(m: int, n: int, k: int) -> Config | None:
+    """The fastest measured config for this GPU and shape, from the largest tuned batch
+    bucket at or below M, or None if nothing has been tuned (reference kernel.py:143-148)."""
+    table = _tuned_table(torch.cuda.get_device_name()).get(f"{k}x{n}", {})
+    fits = [int(bucket) for bucket in table if int(bucket) <= m]
+    return Config(**table[str(max(fits))]["config"]) if fits else None
+
+
+_chosen: dict[tuple[int, int, int, int], Config] = {}
+
+
+def choose_config(m: int, n: int, k: int) -> Config:
+    """tuned_config, else default_config, remembered per device and shape."""
+    key = (torch.cuda.current_device(), m, n, k)
+    cfg = _chosen.get(key)
+    if cfg is None:
+        cfg = _chosen[key] = tuned_config(m, n, k) or default_config(m, n, k)
+    return cfg
+
+
+def supported(m: int, n: int, k: int, config: Config | None = None) -> bool:
+    """Whether w8a8_mm takes (M, N, K) under `config` (default: choose_config)."""
+    cfg = config or default_config(m, n, k)
+    return _lib.lib().i8l_w8a8_mm_supported(m, n, k, _cconfig(cfg)) == _lib.OK
+
+
+def w8a8_mm(
+    a_q: torch.Tensor,
+    b_q: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: torch.Tensor | None = None,
+    *,
+    config: Config | None = None,
+    raw: bool = False,
+    cached_launch: bool = True,
+) -> torch.Tensor:
+    """(A_q @ B_q) * scale_a * scale_b + bias, for int8 A_q [M, K] and B_q [K, N].
+
+    scale_a is per row ([M] or [M, 1]) or a scalar, scale_b per column ([N] or [N, 1]) or
+    a scalar, both float32.  With raw=True the exact int32 product is returned and the
+    scales and bias are ignored.  cached_launch is accepted for API compatibility; every
+    launch is a direct C call already.
+    """
+    if a_q.dtype != torch.int8 or b_q.dtype != torch.int8:
+        raise NotSupported(f"int8 operands only, got {a_q.dtype} and {b_q.dtype}")
+    if a_q.dim() != 2 or b_q.dim() != 2 or a_q.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(a_q.shape)} by {tuple(b_q.shape)}")
+    if not (a_q.is_cuda and b_q.is_cuda):
+        raise NotSupported("operands must be on a HIP device")
+    m, k = a_q.shape
+    n = b_q.shape[1]
+    cfg = config or choose_config(m, n, k)
+    if n % cfg.bn or k % cfg.bk:
+        raise NotSupported(f"N={n} and K={k} must divide the {cfg.name} tile")
+    # Scales and bias are read as flat stride-1 arrays; contiguous() is free when they
+    # already are, and a copy only for a slice or a transpose.
+    sa, sb = scale_a.reshape(-1).contiguous(), scale_b.reshape(-1).contiguous()
+    if sa.dtype != torch.float32 or sb.dtype != torch.float32:
+        raise NotSupported(f"float32 scales only, got {sa.dtype} and {sb.dtype}")
+    if sa.numel() not in (1, m) or sb.numel() not in (1, n):
+        raise ValueError(f"scale sizes {sa.numel()} and {sb.numel()} fit neither {m} nor {n}")
+    if bias is not None and tuple(bias.shape) != (n,):
+        raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
+    if bias is not None:
+        bias = bias.contiguous()
+        bias_code = _lib.DTYPE_CODE.get(bias.dtype)
+        if bias_code not in (_lib.BF16, _lib.F16, _lib.F32):
+            raise NotSupported(f"bias dtype {bias.dtype} is not supported")
+    else:
+        bias_code = _lib.DTYPE_NONE
+    if raw:
+        out_code = _lib.I32
+    else:
+        out_code = _lib.DTYPE_CODE.get(out_dtype)
+        if out_code not in (_lib.BF16, _lib.F16, _lib.F32):
+            raise NotSupported(f"output dtype {out_dtype} is not supported")
+
+    out = torch.empty((m, n), dtype=torch.int32 if raw else out_dtype, device=a_q.device)
+    status = _lib.lib().i8l_w8a8_mm(
+        a_q.data_ptr(), a_q.stride(0), a_q.stride(1),
+        b_q.data_ptr(), b_q.stride(0), b_q.stride(1),
+        sa.data_ptr(), sa.numel(), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code,
+        out.data_ptr(), out.stride(0), out_code,
+        m, n, k, _cconfig(cfg), _lib.stream_of(a_q))
+    _lib.check(status, NotSupported)
+    return out

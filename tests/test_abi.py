@@ -1,0 +1,120 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/*.h declares,
+and its host-only entry points (config choice, the decline rule) behave.  CPU only."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from int8_linear import Config, NotSupported, _lib, default_config, kernel
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(i8l_\w+)\s*\(", text))
+    return names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = declared_symbols()
+    assert declared >= set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+    assert L.i8l_version().decode().startswith("int8_linear_amd")
+
+
+def test_library_binary_is_built_for_gfx950_only():
+    # the offload bundle names its targets; only gfx950 is built
+    data = _lib.LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert b"amdgcn-amd-amdhsa--" + other not in data
+
+
+def test_default_config_regimes():
+    d = default_config(16, 4096, 2048)
+    assert d.stages == 1 and d.bm == 16 and d.bk == 64 * d.warps and 2048 % d.bk == 0
+    assert default_config(17, 4096, 2048).bm == 32          # one tile covers M=17
+    assert default_config(128, 2048, 6144).bm == 128
+    p = default_config(4096, 28672, 4096)
+    assert p.stages == 2 and (p.bm, p.bn) == (256, 256)
+    assert default_config(300, 2048, 2048).stages == 2
+
+
+def test_supported_decline_rule_matches_reference():
+    # kernel.py:228-229 of the reference: N % bn or K % bk declines
+    assert not kernel.supported(4, 64, 100)
+    assert kernel.supported(16, 4096, 2048)
+    assert not kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 3, 1))  # 3 stages: not built
+    assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
+    assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 4, 2, 8))
+    assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 2, 8))
+
+
+def test_supported_reports_the_reason():
+    c = _lib.CConfig(16, 16, 64, 1, 1, 1, 1)
+    assert _lib.lib().i8l_w8a8_mm_supported(4, 64, 100, ctypes.byref(c)) == _lib.UNSUPPORTED
+    assert "must divide" in _lib.last_error()
+    with pytest.raises(NotSupported):
+        _lib.check(_lib.UNSUPPORTED, NotSupported)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.INVALID_ARG, NotSupported)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.HIP_ERROR, NotSupported)
+
+
+def test_invalid_sizes_are_rejected_before_any_launch():
+    L = _lib.lib()
+    st = L.i8l_w8a8_mm(None, 0, 1, None, 1, 0, None, 3, None, 1, None, 0, None, 0, _lib.BF16,
+                       2, 16, 64, None, None)
+    assert st == _lib.INVALID_ARG and "scale_a" in _lib.last_error()
+    st = L.i8l_add_rmsnorm_quant(None, None, None, 1e-6, None, None, None, 1, 8, 7, 1, 1, None)
+    assert st == _lib.UNSUPPORTED
+    # M == 0 launches nothing and succeeds without touching any pointer
+    assert L.i8l_silu_mul_quant(None, None, None, 0, 64, _lib.BF16, 1, 1, None) == _lib.OK
+    assert L.i8l_quant_per_token(None, None, None, 0, 64, _lib.BF16, 1, None) == _lib.OK
+
+
+def test_config_name_format():
+    assert Config(16, 64, 64, 4, 1, 1).name == "16x64x64 w4 s1 g1"
+    assert Config(256, 256, 64, 4, 2, 8, 2).name == "256x256x64 w4 s2 g8 k2"
+
+
+def test_tuned_config_takes_the_largest_bucket_at_or_below_m(monkeypatch):
+    table = {"2048x4096": {"1": {"config": {"bm": 16, "bn": 16, "bk": 512, "warps": 8,
+                                           "stages": 1, "group_m": 1}},
+                           "17": {"config": {"bm": 32, "bn": 16, "bk": 512, "warps": 8,
+                                            "stages": 1, "group_m": 1}}}}
+    monkeypatch.setattr(kernel.torch.cuda, "get_device_name", lambda *a: "TEST GPU")
+    monkeypatch.setattr(kernel, "_tuned_table", lambda name: table if name == "TEST GPU" else {})
+    assert kernel.tuned_config(1, 4096, 2048).bm == 16
+    assert kernel.tuned_config(16, 4096, 2048).bm == 16
+    assert kernel.tuned_config(17, 4096, 2048).bm == 32
+    assert kernel.tuned_config(500, 4096, 2048).bm == 32
+    assert kernel.tuned_config(5, 2048, 2048) is None
+
+
+def test_shipped_tuned_table_is_valid():
+    import json
+    tables = json.loads(kernel.TUNED_PATH.read_text())
+    for device, shapes in tables.items():
+        for kn, buckets in shapes.items():
+            k, n = map(int, kn.split("x"))
+            for m, row in buckets.items():
+                cfg = Config(**row["config"])
+                assert kernel.supported(int(m), n, k, cfg), (device, kn, m, cfg)
+
+
+def test_cpu_tensors_are_declined_not_computed():
+    import torch
+    a = torch.zeros((2, 64), dtype=torch.int8)
+    with pytest.raises(NotSupported):
+        kernel.w8a8_mm(a, torch.zeros((64, 16), dtype=torch.int8), torch.ones(1), torch.ones(1))

@@ -1,0 +1,239 @@
+"""W8A8 GEMM on the GPU against the CPU oracle, through the C ABI.
+
+The cases mirror the reference's tests/test_kernel.py (AshrithaG/int8-linear): exact int32
+products at ragged and even M (41-45), other tilings (48-53), scaled outputs against
+float64 (56-75), the decline rule (78-82), graph replay (85-100) and an odd data pointer
+(139-145).  Beyond them: every output is compared with the oracle bit for bit, the BASELINE
+decode sweep (configs 0-1) at full size, and the prefill shapes (config 3) at full size
+through size-independent checks (row and column checksums of the int32 product, plus full
+rows compared exactly).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, ints, np_, offset_ints, say
+from int8_linear import Config, NotSupported, w8a8_mm
+from int8_linear.operands import operands, seed_of
+from int8_linear.shapes import SHAPES
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+CODE = {torch.bfloat16: o.BF16, torch.float16: o.F16, torch.float32: o.F32}
+
+
+def oracle_out(a, w, sa, sb, bias, dtype):
+    acc = o.gemm_i32(np_(a), np_(w))
+    if bias is None:
+        bias_np, bdt = None, o.NONE
+    elif bias.dtype == torch.float32:
+        bias_np, bdt = np_(bias), o.F32
+    else:
+        bias_np, bdt = bits(bias), CODE[bias.dtype]
+    return o.epilogue(acc, np_(sa), np_(sb), bias_np, bdt, CODE[dtype])
+
+
+def as_np(out: torch.Tensor) -> np.ndarray:
+    return np_(out) if out.dtype in (torch.float32, torch.int32) else bits(out)
+
+
+SHAPES_REF = [(1, 2048, 2048), (3, 2048, 1024), (17, 2048, 6144), (64, 2048, 2048),
+              (100, 6144, 2048)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES_REF)
+def test_int32_product_is_exact(m, k, n):
+    say(f"w8a8_mm raw m={m} k={k} n={n}")
+    a, w = ints((m, k), 1), ints((n, k), 2)
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, w.t(), one, one, raw=True)
+    ref = o.gemm_i32(np_(a), np_(w))
+    assert got.dtype == torch.int32 and np.array_equal(np_(got), ref)
+    assert np.array_equal(ref, (np_(a).astype(np.float64) @ np_(w).astype(np.float64).T).astype(np.int32))
+
+
+TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64, 16, 512, 8, 1, 1),
+           Config(128, 16, 256, 4, 1, 1), Config(16, 32, 512, 8, 1, 1),
+           Config(128, 128, 64, 4, 2, 8), Config(256, 128, 64, 4, 2, 1),
+           Config(128, 256, 64, 4, 2, 1), Config(256, 256, 64, 4, 2, 8),
+           Config(256, 256, 128, 4, 2, 8), Config(128, 128, 128, 4, 2, 1)]
+
+
+@pytest.mark.parametrize("config", TILINGS, ids=lambda c: c.name.replace(" ", "_"))
+@pytest.mark.parametrize("m", [256, 300])
+def test_exact_under_other_tilings(config, m):
+    k, n = 2048, 1024
+    say(f"w8a8_mm raw m={m} k={k} n={n} config={config.name}")
+    a, w = ints((m, k), 3), ints((n, k), 4)
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, w.t(), one, one, raw=True, config=config)
+    assert np.array_equal(np_(got), o.gemm_i32(np_(a), np_(w)))
+    # and the scaled path of the same tiling
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config)
+    assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("per_row", [True, False])
+@pytest.mark.parametrize("per_col", [True, False])
+@pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float16, torch.float32])
+def test_scaled_output_matches_oracle_and_float64(dtype, per_row, per_col, bias_dtype):
+    m, k, n = 37, 2048, 1024
+    say(f"w8a8_mm scaled m={m} {dtype} row={per_row} col={per_col} bias={bias_dtype}")
+    a, w = ints((m, k), 5), ints((n, k), 6)
+    g = torch.Generator().manual_seed(7)
+    sa = (torch.rand((m, 1) if per_row else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+    sb = (torch.rand((n, 1) if per_col else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+    bias = torch.randn(n, generator=g).to(bias_dtype).cuda() if bias_dtype else None
+    got = w8a8_mm(a, w.t(), sa, sb, dtype, bias)
+    assert got.dtype == dtype
+    assert np.array_equal(as_np(got), oracle_out(a, w, sa, sb, bias, dtype))
+    # the reference's own check (tests/test_kernel.py:68-75): rel < 1e-2 of max(|ref|,|term|)
+    term = (np_(a).astype(np.float64) @ np_(w).astype(np.float64).T) * \
+        np_(sa).astype(np.float64).reshape(-1, 1) * np_(sb).astype(np.float64).reshape(1, -1)
+    ref = term + np_(bias.float()).astype(np.float64) if bias is not None else term
+    scale = np.maximum(np.abs(ref), np.abs(term)).clip(1e-6)
+    assert (np.abs(np_(got.float()).astype(np.float64) - ref) / scale).max() < 1e-2
+    if bias is None and dtype == torch.bfloat16:
+        # within one bf16 ulp of float64
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+        assert np.all(np.abs(np_(got.float()).astype(np.float64) - ref) <= ulp)
+
+
+def test_declines_shapes_the_tiles_do_not_divide():
+    a, w = ints((4, 100), 8), ints((64, 100), 9)
+    one = torch.ones(1, device="cuda")
+    with pytest.raises(NotSupported):
+        w8a8_mm(a, w.t(), one, one)
+
+
+def test_replays_inside_a_hip_graph():
+    m, k, n = 16, 2048, 2048
+    say("w8a8_mm graph capture m=16")
+    a, w = ints((m, k), 10), ints((n, k), 11)
+    sa = torch.full((m, 1), 1e-2, device="cuda")
+    sb = torch.full((n, 1), 1e-2, device="cuda")
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        w8a8_mm(a, w.t(), sa, sb)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = w8a8_mm(a, w.t(), sa, sb)
+    for seed in (12, 13, 14):
+        a.copy_(ints((m, k), seed))  # new input in the same buffer
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = w8a8_mm(a, w.t(), sa, sb)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager)
+        assert np.array_equal(bits(eager), oracle_out(a, w, sa, sb, None, torch.bfloat16))
+
+
+def test_exact_on_an_odd_pointer():
+    m, k, n = 5, 2048, 1024
+    say("w8a8_mm odd A pointer (generic schedule)")
+    a, w = offset_ints((m, k), 23), ints((n, k), 24)
+    assert a.data_ptr() % 2 == 1
+    one = torch.ones(1, device="cuda")
+    for _ in range(3):
+        assert np.array_equal(np_(w8a8_mm(a, w.t(), one, one, raw=True)), o.gemm_i32(np_(a), np_(w)))
+
+
+def test_exact_on_an_n_contiguous_weight():
+    m, k, n = 9, 256, 48
+    say("w8a8_mm N-contiguous B (generic schedule)")
+    a = ints((m, k), 25)
+    b = ints((k, n), 26)                      # [K, N] row-major: stride (N, 1)
+    sa = torch.rand((m, 1), device="cuda") + 0.5
+    sb = torch.rand((n, 1), device="cuda") + 0.5
+    got = w8a8_mm(a, b, sa, sb, torch.float32)
+    w = b.t().contiguous()
+    assert np.array_equal(np_(got), oracle_out(a, w, sa, sb, None, torch.float32))
+
+
+def test_empty_batch():
+    a = torch.empty((0, 2048), dtype=torch.int8, device="cuda")
+    w = ints((1024, 2048), 1)
+    out = w8a8_mm(a, w.t(), torch.ones(1, device="cuda"), torch.ones(1, device="cuda"))
+    assert out.shape == (0, 1024)
+
+
+def test_golden_fixtures():
+    from pathlib import Path
+    gdir = Path(__file__).resolve().parent / "golden"
+    for name in ("gemm_small", "gemm_config0"):
+        say(f"w8a8_mm golden {name}")
+        f = np.load(gdir / f"{name}.npz")
+        a = torch.from_numpy(f["a"]).cuda()
+        w = torch.from_numpy(f["w"]).cuda()
+        sa, sb = torch.from_numpy(f["sa"]).cuda(), torch.from_numpy(f["sb"]).cuda()
+        one = torch.ones(1, device="cuda")
+        assert np.array_equal(np_(w8a8_mm(a, w.t(), one, one, raw=True)), f["raw"])
+        assert np.array_equal(bits(w8a8_mm(a, w.t(), sa, sb)), f["out_bf16"])
+        bias = torch.from_numpy(f["bias_bf16"].view(np.int16)).view(torch.bfloat16).cuda()
+        key = "out_bf16_bias_bf16" if name == "gemm_small" else "out_bf16_bias"
+        assert np.array_equal(bits(w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, bias)), f[key])
+        if name == "gemm_small":
+            bf = torch.from_numpy(f["bias_f32"]).cuda()
+            assert np.array_equal(bits(w8a8_mm(a, w.t(), sa, sb, torch.float16, bf)),
+                                  f["out_f16_bias_f32"])
+            out = w8a8_mm(a, w.t(), sa[:1, :1].reshape(1), sb[:1, :1].reshape(1), torch.float32)
+            assert np.array_equal(np_(out), f["out_f32_scalar"])
+
+
+# the four Qwen3-1.7B shapes at every decode M, bias off and on.
+DECODE_M = [1, 2, 4, 8, 16, 17, 32, 64, 128]
+
+
+@pytest.mark.parametrize("shape", SHAPES["qwen3-1.7b-vllm"], ids=lambda s: s[0])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_decode_sweep_is_bit_exact(shape, with_bias):
+    _, k, n = shape
+    for m in DECODE_M:
+        say(f"decode sweep {shape[0]} m={m} bias={with_bias}")
+        d = operands(m, k, n, seed_of(m, k, n), with_bias=with_bias, device="cuda")
+        got = w8a8_mm(d["a_q"], d["w_qt"], d["a_s"], d["w_s"], torch.bfloat16, d["bias"])
+        ref = oracle_out(d["a_q"], d["w_q"], d["a_s"], d["w_s"], d["bias"], torch.bfloat16)
+        assert np.array_equal(bits(got), ref), (shape, m, with_bias)
+
+
+def matvec(w: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """Exact int64 W[N,K] @ v[K] in row chunks (no full int64 copy of W)."""
+    return np.concatenate([w[i:i + 2048].astype(np.int64) @ v for i in range(0, w.shape[0], 2048)])
+
+
+# Llama-3-8B shapes at prefill M, full size.
+@pytest.mark.parametrize("shape", SHAPES["llama-3-8b"], ids=lambda s: s[0])
+def test_prefill_full_size_checksums_and_rows(shape):
+    _, k, n = shape
+    rng = np.random.default_rng(k + n)
+    w = ints((n, k), k * 7 + n)
+    w_np = np_(w)
+    wsum_k = w_np.sum(axis=0, dtype=np.int64)     # [K]: sum over n of W[n, k]
+    one = torch.ones(1, device="cuda")
+    for m in (512, 1024, 2048, 4096):
+        say(f"prefill {shape[0]} m={m} k={k} n={n}")
+        a = ints((m, k), m + k)
+        a_np = np_(a).astype(np.int64)
+        got = w8a8_mm(a, w.t(), one, one, raw=True)
+        # row checksums: sum_n C[m,n] = A[m,:] . (sum_n W[n,:]); column checksums likewise
+        assert np.array_equal(np_(got.sum(dim=1, dtype=torch.int64)), a_np @ wsum_k)
+        assert np.array_equal(np_(got.sum(dim=0, dtype=torch.int64)), matvec(w_np, a_np.sum(axis=0)))
+        rows = np.sort(rng.choice(m, 6, replace=False))
+        rows = np.concatenate([rows, [0, m - 1]])
+        got_rows = np_(got[torch.from_numpy(rows).cuda()])
+        assert np.array_equal(got_rows, o.gemm_i32(np_(a)[rows], np_(w)))
+        # scaled path, same rows against the oracle epilogue
+        sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+        sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+        out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16)
+        ref = o.epilogue(got_rows, np_(sa)[rows], np_(sb), None, o.NONE, o.BF16)
+        assert np.array_equal(bits(out[torch.from_numpy(rows).cuda()]), ref)
+        del got, out

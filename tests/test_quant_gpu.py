@@ -1,0 +1,223 @@
+"""The fused quantizer kernels on the GPU against the CPU oracle, through the C ABI.
+
+The cases mirror the reference's tests/test_fused_quant.py (AshrithaG/int8-linear):
+add+RMSNorm+quant at five (M, K) with and without the residual (64-75), SiLU-and-mul+quant
+at three (M, I) with and without SiLU rounding (78-83), the zero row (86-90), saturation
+(93-97) and opcheck of the custom ops (100-105).  Every code, scale and residual is compared
+with the oracle bit for bit, and with the reference's torch restatement under its own
+tolerance; BASELINE config 2 (H=2048, I=6144, M up to 4096) runs at full size.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, from_bits, np_, randn, say
+from int8_linear import fused_quant as fq
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+CODE = {torch.bfloat16: o.BF16, torch.float16: o.F16}
+
+
+def ref_quant(yf):
+    absmax = yf.abs().amax(-1, keepdim=True)
+    inv = torch.where(absmax == 0, torch.zeros_like(absmax), 127.0 / absmax)
+    return torch.round(yf * inv).clamp(-128, 127).to(torch.int8), absmax / 127.0
+
+
+def ref_norm(x, r, w):
+    """The reference's torch restatement (tests/test_fused_quant.py:34-43), on the CPU."""
+    x, w = x.cpu(), w.cpu()
+    xf = x.float()
+    rout = None
+    if r is not None:
+        xf = xf + r.cpu().float()
+        rout = xf.to(x.dtype)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    y = ((xf * torch.rsqrt(var + EPS)).to(w.dtype) * w).to(x.dtype)
+    return (*ref_quant(y.float()), rout)
+
+
+def ref_silu(gu, round_silu):
+    gu = gu.cpu()
+    i = gu.shape[1] // 2
+    g, u = gu[:, :i].float(), gu[:, i:].float()
+    a = g / (1.0 + torch.exp(-g))
+    if round_silu:
+        a = a.to(gu.dtype).float()
+    return ref_quant((a * u).to(gu.dtype).float())
+
+
+def assert_close_int8(q, s, q0, s0):
+    d = (q.cpu().int() - q0.int()).abs()
+    assert d.max().item() <= 1
+    assert d.ne(0).sum().item() <= max(8, 1e-3 * d.numel())
+    assert ((s.cpu() - s0).abs() / s0.clamp_min(1e-30)).max().item() < 1e-5
+
+
+def check_norm(x, r, w, precise=True):
+    q, s, rout = fq.add_rmsnorm_quant(x, r, w, EPS, precise_div=precise)
+    q0, s0, r0 = o.add_rmsnorm_quant(bits(x), None if r is None else bits(r), bits(w), EPS,
+                                     CODE[x.dtype], CODE[w.dtype], precise)
+    assert np.array_equal(np_(q), q0)
+    assert np.array_equal(np_(s), s0)
+    if r is not None:
+        assert np.array_equal(bits(rout), r0)
+    else:
+        assert rout is None
+    return q, s, rout
+
+
+@pytest.mark.parametrize("m,k", [(1, 2048), (7, 2048), (64, 1024), (300, 2048), (5, 1000),
+                                 (3, 13), (2, 6144)])
+@pytest.mark.parametrize("has_res", [False, True])
+def test_add_rmsnorm_quant(m, k, has_res):
+    say(f"add_rmsnorm_quant m={m} k={k} res={has_res}")
+    x = randn((m, k), m)
+    r = randn((m, k), m + 1) if has_res else None
+    w = randn((k,), 99, 0.1) + 1.0
+    q, s, rout = check_norm(x, r, w)
+    q0, s0, r0 = ref_norm(x, r, w)
+    assert_close_int8(q, s, q0, s0)
+    if has_res:
+        assert torch.equal(rout.cpu(), r0)                  # the residual stream must not drift
+    assert q.dtype == torch.int8 and s.shape == (m, 1)
+
+
+@pytest.mark.parametrize("m", [1, 16, 128, 1024, 4096])
+def test_add_rmsnorm_quant_config2(m):
+    say(f"add_rmsnorm_quant config2 m={m}")
+    x, r = randn((m, 2048), 10 + m), randn((m, 2048), 20 + m)
+    w = randn((2048,), 98, 0.1) + 1.0
+    check_norm(x, r, w)
+    check_norm(x, None, w)
+
+
+def test_add_rmsnorm_quant_fp16_and_approximate_division():
+    say("add_rmsnorm_quant fp16")
+    x = randn((9, 2048), 1, dtype=torch.float16)
+    r = randn((9, 2048), 2, dtype=torch.float16)
+    w = randn((2048,), 3, 0.1, dtype=torch.float16) + 1.0
+    check_norm(x, r, w)
+    check_norm(x, r, w, precise=False)
+    wb = randn((2048,), 4, 0.1) + 1.0                       # bf16 weight, fp16 activations
+    check_norm(x, r, wb)
+
+
+def check_silu(gu, round_silu, precise=True):
+    q, s = fq.silu_mul_quant(gu, precise_div=precise, round_silu=round_silu)
+    q0, s0 = o.silu_mul_quant(bits(gu), CODE[gu.dtype], round_silu, precise)
+    assert np.array_equal(np_(q), q0) and np.array_equal(np_(s), s0)
+    return q, s
+
+
+@pytest.mark.parametrize("m,i", [(1, 6144), (33, 6144), (8, 1000), (3, 13), (2, 12000)])
+@pytest.mark.parametrize("round_silu", [False, True])
+def test_silu_mul_quant(m, i, round_silu):
+    say(f"silu_mul_quant m={m} i={i} round={round_silu}")
+    gu = randn((m, 2 * i), m, 2.0)
+    q, s = check_silu(gu, round_silu)
+    assert_close_int8(q, s, *ref_silu(gu, round_silu))
+
+
+@pytest.mark.parametrize("m", [1, 16, 128, 1024, 4096])
+def test_silu_mul_quant_config2(m):
+    say(f"silu_mul_quant config2 m={m}")
+    gu = randn((m, 12288), 30 + m)
+    check_silu(gu, True)
+    check_silu(gu, False, precise=False)
+
+
+@pytest.mark.parametrize("m,k", [(1, 2048), (16, 2048), (4096, 2048), (3, 13)])
+def test_quant_per_token(m, k):
+    say(f"quant_per_token m={m} k={k}")
+    x = randn((m, k), 40 + m, 3.0)
+    q, s = fq.quant_per_token(x)
+    q0, s0 = o.quant_per_token(bits(x))
+    assert np.array_equal(np_(q), q0) and np.array_equal(np_(s), s0)
+    qr, sr = ref_quant(x.cpu().float())
+    assert torch.equal(q.cpu(), qr) and torch.equal(s.cpu(), sr)
+
+
+def test_zero_row_gives_zero_scale_and_values():
+    x = torch.zeros((3, 2048), device="cuda", dtype=torch.bfloat16)
+    w = torch.ones(2048, device="cuda", dtype=torch.bfloat16)
+    q, s, _ = fq.add_rmsnorm_quant(x, None, w, EPS)
+    assert q.abs().max().item() == 0 and s.abs().max().item() == 0
+    q, s = fq.quant_per_token(x)
+    assert q.abs().max().item() == 0 and s.abs().max().item() == 0
+
+
+def test_saturates_at_127():
+    """The largest-magnitude element of every row must land on +-127 exactly."""
+    gu = randn((16, 2 * 512), 5, 3.0)
+    q, _ = fq.silu_mul_quant(gu)
+    assert q.int().abs().amax(-1).eq(127).all()
+
+
+def test_empty_batch():
+    x = torch.empty((0, 2048), device="cuda", dtype=torch.bfloat16)
+    w = torch.ones(2048, device="cuda", dtype=torch.bfloat16)
+    q, s, rout = fq.add_rmsnorm_quant(x, x, w, EPS)
+    assert q.shape == (0, 2048) and s.shape == (0, 1) and rout.shape == (0, 2048)
+    q, s = fq.silu_mul_quant(torch.empty((0, 64), device="cuda", dtype=torch.bfloat16))
+    assert q.shape == (0, 32)
+
+
+def test_golden_fixtures():
+    say("quantizers golden fixtures")
+    f = np.load(Path(__file__).resolve().parent / "golden" / "quantizers.npz")
+    x, r, g = from_bits(f["x"]), from_bits(f["r"]), from_bits(f["gamma"])
+    q, s, rout = fq.add_rmsnorm_quant(x, r, g, EPS)
+    assert np.array_equal(np_(q), f["q_res"]) and np.array_equal(np_(s), f["s_res"])
+    assert np.array_equal(bits(rout), f["rout"])
+    q, s, _ = fq.add_rmsnorm_quant(x, None, g, EPS)
+    assert np.array_equal(np_(q), f["q_nores"]) and np.array_equal(np_(s), f["s_nores"])
+    gu = from_bits(f["gu"])
+    for key, rs in (("silu", False), ("silu_round", True)):
+        q, s = fq.silu_mul_quant(gu, round_silu=rs)
+        assert np.array_equal(np_(q), f[f"q_{key}"]) and np.array_equal(np_(s), f[f"s_{key}"])
+    q, s = fq.quant_per_token(from_bits(f["xp"]))
+    assert np.array_equal(np_(q), f["q_plain"]) and np.array_equal(np_(s), f["s_plain"])
+
+
+def test_custom_ops_opcheck():
+    x, r = randn((9, 2048), 1), randn((9, 2048), 2)
+    w = randn((2048,), 3) + 1.0
+    torch.library.opcheck(fq.rmsnorm_quant_op, (x, w, EPS))
+    torch.library.opcheck(fq.add_rmsnorm_quant_op, (x, r, w, EPS))
+    torch.library.opcheck(fq.silu_mul_quant_op, (randn((9, 2 * 6144), 4),))
+    torch.library.opcheck(fq.quant_per_token_op, (x,))
+
+
+def test_quantizers_replay_inside_a_hip_graph():
+    say("quantizers graph capture")
+    x, r = randn((16, 2048), 50), randn((16, 2048), 51)
+    w = randn((2048,), 52, 0.1) + 1.0
+    gu = randn((16, 12288), 53)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        fq.add_rmsnorm_quant(x, r, w, EPS)
+        fq.silu_mul_quant(gu, True, True)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        q1, s1, r1 = fq.add_rmsnorm_quant(x, r, w, EPS)
+        q2, s2 = fq.silu_mul_quant(gu, True, True)
+    for seed in (60, 61):
+        x.copy_(randn((16, 2048), seed))
+        gu.copy_(randn((16, 12288), seed + 100))
+        graph.replay()
+        torch.cuda.synchronize()
+        e1 = fq.add_rmsnorm_quant(x, r, w, EPS)
+        e2 = fq.silu_mul_quant(gu, True, True)
+        torch.cuda.synchronize()
+        assert torch.equal(q1, e1[0]) and torch.equal(s1, e1[1]) and torch.equal(r1, e1[2])
+        assert torch.equal(q2, e2[0]) and torch.equal(s2, e2[1])
