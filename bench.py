@@ -97,32 +97,38 @@ def check_linear(out, d) -> float:
 
 
 class Sweep:
-    """The decode sweep's operands, with weight copies rotated across calls."""
+    """The decode sweep's operands.  Each shape has one weight (seeded as the benchmark's
+    M=16 point) held in several copies that calls rotate through; each (M, bias) point
+    has its own seeded activations and bias."""
 
     def __init__(self, shapes, ms, device):
         import torch
 
         from int8_linear.operands import operands, seed_of
-        self.points = []   # (label, m, k, n, bias, operand dict)
+        per_set = sum(k * n for _, k, n in shapes)
+        self.copies = max(2, -(-ROTATE_BYTES // per_set))
+        self.weights = {}   # (k, n) -> ([w_q copies], w_s)
+        for _, k, n in shapes:
+            d = operands(16, k, n, seed_of(16, k, n), device=device)
+            self.weights[(k, n)] = ([d["w_q"]] + [d["w_q"].clone() for _ in range(self.copies - 1)],
+                                    d["w_s"])
+        self.points = []    # (label, m, k, n, bias, operand dict)
         for label, k, n in shapes:
             for m in ms:
                 for bias in (False, True):
                     d = operands(m, k, n, seed_of(m, k, n), with_bias=bias, device=device)
+                    d["w_q"], d["w_s"] = self.weights[(k, n)][0][0], self.weights[(k, n)][1]
+                    del d["w_qt"], d["w"]
                     self.points.append((label, m, k, n, bias, d))
-        per_set = sum(k * n for _, k, n in shapes)
-        self.copies = max(2, -(-ROTATE_BYTES // per_set))
-        base = {(k, n): self.points[[p[2:4] for p in self.points].index((k, n))][5]["w_q"]
-                for _, k, n in shapes}
-        self.weights = {kn: [w] + [w.clone() for _ in range(self.copies - 1)]
-                        for kn, w in base.items()}
         torch.cuda.synchronize()
 
     def call(self, idx: int, copy: int):
         from int8_linear import w8a8_mm
         import torch
         label, m, k, n, bias, d = self.points[idx]
-        w = self.weights[(k, n)][copy % self.copies]
-        return w8a8_mm(d["a_q"], w.t(), d["a_s"], d["w_s"], torch.bfloat16, d["bias"])
+        ws, w_s = self.weights[(k, n)]
+        return w8a8_mm(d["a_q"], ws[copy % self.copies].t(), d["a_s"], w_s, torch.bfloat16,
+                       d["bias"])
 
 
 def cpu_baseline() -> dict:

@@ -47,26 +47,49 @@ struct Cols4 {
   float sb[4], bias[4];
 };
 
+// Branch-free loads of the epilogue operands of columns n..n+3: every address is chosen
+// with a select from pointers that are always valid (a scalar scale is re-read with stride
+// 0; an absent bias re-reads scale_b), and every bias dtype is read as 16-bit halves, so
+// all loads issue in one basic block and their latency is paid once.
 __device__ __forceinline__ Cols4 load_cols4(const Epi& e, int64_t n) {
   Cols4 c;
   if (e.out_dtype == I8L_I32) return c;
+  const int64_t sbs = e.sb_per_col ? 1 : 0;
+  const bool f32b = e.bias_dtype == I8L_F32;
+  const bool hasb = e.bias_dtype != I8L_DTYPE_NONE;
+  const uint16_t* bb = hasb ? (const uint16_t*)e.bias : (const uint16_t*)e.sb;
+  const int64_t bstep = hasb ? (f32b ? 2 : 1) : 0;
+  uint32_t lo[4], hi[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    c.sb[r] = e.sb[e.sb_per_col ? n + r : 0];
-    c.bias[r] = e.bias_dtype != I8L_DTYPE_NONE ? load_bias(e.bias, e.bias_dtype, n + r) : 0.0f;
+    c.sb[r] = e.sb[(n + r) * sbs];
+    const uint16_t* p = bb + (n + r) * bstep;
+    lo[r] = p[0];
+    hi[r] = p[f32b ? 1 : 0];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float fb = __uint_as_float(lo[r] | (hi[r] << 16));
+    const float bf = bf16_bits_to_f32(lo[r]);
+    const float hf = f16_bits_to_f32(lo[r]);
+    c.bias[r] = !hasb ? 0.0f : f32b ? fb : e.bias_dtype == I8L_BF16 ? bf : hf;
   }
   return c;
 }
 
 // Four consecutive output columns n..n+3 of row m (n a multiple of 4; the fast schedules
 // require a 16-byte aligned output with 16-byte aligned rows).
-__device__ __forceinline__ void store4c(const Epi& e, int64_t m, int64_t n, v4i acc,
-                                        const Cols4& c) {
+__device__ __forceinline__ float load_sa(const Epi& e, int64_t m) {
+  if (e.out_dtype == I8L_I32) return 0.0f;
+  return e.sa[m * (e.sa_per_row ? 1 : 0)];
+}
+
+__device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i acc,
+                                        const Cols4& c, float sam) {
   if (e.out_dtype == I8L_I32) {
     *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
     return;
   }
-  const float sam = e.sa[e.sa_per_row ? m : 0];
   float o[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -91,6 +114,11 @@ __device__ __forceinline__ void store4c(const Epi& e, int64_t m, int64_t n, v4i 
   }
 }
 
+__device__ __forceinline__ void store4c(const Epi& e, int64_t m, int64_t n, v4i acc,
+                                        const Cols4& c) {
+  store4s(e, m, n, acc, c, load_sa(e, m));
+}
+
 __device__ __forceinline__ void store4(const Epi& e, int64_t m, int64_t n, v4i acc) {
   store4c(e, m, n, acc, load_cols4(e, n));
 }
@@ -113,6 +141,10 @@ __device__ __forceinline__ void store1(const Epi& e, int64_t m, int64_t n, int32
 }
 
 __device__ __forceinline__ v4i ld16(const int8_t* p) { return *(const v4i*)p; }
+// Weight bytes are read exactly once per call: stream them past the caches.
+__device__ __forceinline__ v4i ld16_stream(const int8_t* p) {
+  return __builtin_nontemporal_load((const v4i*)p);
+}
 
 // ------------------------------------------------------------------ stream schedule
 // Workgroup = W waves on the same 16*NT output columns and 16*MT tokens; wave w owns the
@@ -128,7 +160,10 @@ __host__ __device__ constexpr int stream_max_threads(int mt, int nt) {
   return 2 * stream_unroll(mt, nt) * (mt + nt) * 4 + mt * nt * 4 <= 80 ? 1024 : 512;
 }
 
-template <int MT, int NT, int U>
+// NC (16, 8 or 4) output columns per MFMA tile: with NC < 16, MFMA rows i and i+NC read
+// the same weight row (the loads coalesce, so HBM traffic is unchanged) and only rows
+// below NC are stored.  Narrow tiles give narrow-N shapes more workgroups.
+template <int MT, int NT, int U, int NC>
 __global__ void __launch_bounds__(stream_max_threads(MT, NT))
 gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
             int64_t ldb, Epi e, int ks) {
@@ -136,20 +171,18 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   const int wave = threadIdx.x >> 6;
   const int W = blockDim.x >> 6;
   const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * (16 * NT);
+  const int64_t n0 = (int64_t)blockIdx.x * (NC * NT);
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
   const int64_t kbeg = (int64_t)wave * ks * 64 + grp * 16;
 
   const int8_t* bp[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) bp[t] = B + (n0 + 16 * t + r16) * ldb + kbeg;
+  for (int t = 0; t < NT; ++t) bp[t] = B + (n0 + NC * t + r16 % NC) * ldb + kbeg;
   const int8_t* ap[MT];
-  bool aok[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int64_t m = m0 + 16 * i + r16;
-    aok[i] = m < e.M;
-    ap[i] = A + (aok[i] ? m : 0) * lda + kbeg;
+    ap[i] = A + (m < e.M ? m : 0) * lda + kbeg;
   }
 
   v4i acc[MT][NT];
@@ -158,48 +191,61 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[i][t] = v4i{0, 0, 0, 0};
 
-  v4i cb[U][NT], ca[U][MT];
+  // Two register buffers of U steps each, used in turn (no copies between them, so the
+  // wait before each group's MFMAs covers exactly that group's loads).  Padding token
+  // rows load row 0's bytes: their output columns are computed but never stored.
+  v4i b0[U][NT], a0[U][MT], b1[U][NT], a1[U][MT];
+  auto load = [&](v4i (&bb)[U][NT], v4i (&aa)[U][MT], int s) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) cb[u][t] = ld16(bp[t] + u * 64);
+      for (int t = 0; t < NT; ++t) bb[u][t] = ld16_stream(bp[t] + (s + u) * 64);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) ca[u][i] = aok[i] ? ld16(ap[i] + u * 64) : v4i{0, 0, 0, 0};
-  }
-  for (int s = 0; s < ks; s += U) {
-    v4i nb[U][NT], na[U][MT];
-    const bool more = s + U < ks;
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) nb[u][t] = ld16(bp[t] + (s + U + u) * 64);
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-          na[u][i] = aok[i] ? ld16(ap[i] + (s + U + u) * 64) : v4i{0, 0, 0, 0};
-      }
+      for (int i = 0; i < MT; ++i) aa[u][i] = ld16(ap[i] + (s + u) * 64);
     }
+    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any MFMA waits
+  };
+  auto mma = [&](const v4i (&bb)[U][NT], const v4i (&aa)[U][MT]) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cb[u][t], ca[u][i], acc[i][t], 0, 0, 0);
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) cb[u][t] = nb[u][t];
-#pragma unroll
-        for (int i = 0; i < MT; ++i) ca[u][i] = na[u][i];
-      }
-    }
+          acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bb[u][t], aa[u][i], acc[i][t], 0, 0, 0);
+  };
+  // Steady state: every load unconditional, so at each wait exactly the group after the
+  // one being consumed is still in flight on every path.
+  const int G = ks / U;  // groups of U steps
+  load(b0, a0, 0);
+  // The wave that stores fragment f (f % W == wave) loads its scales and bias now, behind
+  // the first weight group, so their latency is hidden by the main loop.
+  constexpr int F = MT * NT;
+  Cols4 cl0;
+  float sa0 = 0.0f;
+  if (wave < F && 4 * grp < NC) {
+    const int i = wave / NT, t = wave % NT;
+    const int64_t m = m0 + 16 * i + r16;
+    cl0 = load_cols4(e, n0 + NC * t + 4 * grp);
+    sa0 = load_sa(e, m < e.M ? m : 0);
+  }
+  int g = 0;
+  for (; g + 2 < G; g += 2) {
+    load(b1, a1, (g + 1) * U);
+    mma(b0, a0);
+    load(b0, a0, (g + 2) * U);
+    mma(b1, a1);
+  }
+  if (G - g == 2) {
+    load(b1, a1, (g + 1) * U);
+    mma(b0, a0);
+    mma(b1, a1);
+  } else {
+    mma(b0, a0);
   }
 
   // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
   extern __shared__ v4i red[];  // [W][MT*NT][64]
-  constexpr int F = MT * NT;
   if (W > 1) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -223,7 +269,12 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
     }
     const int i = f / NT, t = f % NT;
     const int64_t m = m0 + 16 * i + r16;
-    if (m < e.M) store4(e, m, n0 + 16 * t + 4 * grp, s);
+    if (m < e.M && 4 * grp < NC) {
+      if (f == wave)
+        store4s(e, m, n0 + NC * t + 4 * grp, s, cl0, sa0);
+      else
+        store4(e, m, n0 + NC * t + 4 * grp, s);
+    }
   }
 }
 
@@ -373,23 +424,26 @@ gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_
 namespace {
 
 struct StreamTile {
-  int mt, nt;
+  int mt, nt, nc;
 };
 struct StagedTile {
   int bm, bn, bk, wm, wn;
 };
 
 // The tiles this library is built with.
-constexpr StreamTile kStream[] = {{1, 1}, {2, 1}, {4, 1}, {8, 1}, {1, 2}, {2, 2}, {4, 2}};
+// (MT, NT, NC): bm = 16*MT tokens, bn = NC*NT columns.  NC < 16 only with NT == 1, so bn
+// names the tile unambiguously.
+constexpr StreamTile kStream[] = {{1, 1, 16}, {2, 1, 16}, {4, 1, 16}, {8, 1, 16}, {1, 2, 16},
+                                  {2, 2, 16}, {4, 2, 16}, {1, 1, 8},  {2, 1, 8},  {1, 1, 4}};
 constexpr StagedTile kStaged[] = {{128, 128, 64, 2, 2},  {256, 128, 64, 2, 2},
                                   {128, 256, 64, 2, 2},  {256, 256, 64, 2, 2},
                                   {256, 256, 128, 2, 2}, {128, 128, 128, 2, 2}};
 
 bool stream_ok(const i8l_config& c) {
-  if (c.stages != 1 || c.split_k != 1 || c.bm % 16 || c.bn % 16) return false;
+  if (c.stages != 1 || c.split_k != 1 || c.bm % 16) return false;
   if (c.warps < 1 || c.bk != 64 * c.warps) return false;
   for (auto t : kStream)
-    if (t.mt * 16 == c.bm && t.nt * 16 == c.bn) {
+    if (t.mt * 16 == c.bm && t.nt * t.nc == c.bn) {
       const int f = t.mt * t.nt;
       return c.warps * 64 <= stream_max_threads(t.mt, t.nt) &&
              (c.warps == 1 || c.warps * f * 1024 <= 96 * 1024);
@@ -406,28 +460,30 @@ int staged_index(const i8l_config& c) {
   return -1;
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int NC>
 hipError_t launch_stream_u(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                            const Epi& e, int W, int ks, hipStream_t st) {
-  const dim3 grid(e.N / (16 * NT), (e.M + 16 * MT - 1) / (16 * MT));
+  const dim3 grid(e.N / (NC * NT), (e.M + 16 * MT - 1) / (16 * MT));
   const size_t shm = W > 1 ? (size_t)W * MT * NT * 1024 : 0;
   constexpr int UMAX = stream_unroll(MT, NT);
   if (UMAX == 4 && ks % 4 == 0)
-    hipLaunchKernelGGL((gemm_stream<MT, NT, UMAX>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, UMAX, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
   else if (ks % 2 == 0)
-    hipLaunchKernelGGL((gemm_stream<MT, NT, 2>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 2, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
   else
-    hipLaunchKernelGGL((gemm_stream<MT, NT, 1>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 1, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
   return hipGetLastError();
 }
 
 hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int K, hipStream_t st) {
-  const int mt = c.bm / 16, nt = c.bn / 16, W = c.warps, ks = K / (64 * W);
-#define I8L_STREAM(MT_, NT_) \
-  if (mt == MT_ && nt == NT_) return launch_stream_u<MT_, NT_>(a, lda, b, ldb, e, W, ks, st);
-  I8L_STREAM(1, 1) I8L_STREAM(2, 1) I8L_STREAM(4, 1) I8L_STREAM(8, 1)
-  I8L_STREAM(1, 2) I8L_STREAM(2, 2) I8L_STREAM(4, 2)
+  const int mt = c.bm / 16, bn = c.bn, W = c.warps, ks = K / (64 * W);
+#define I8L_STREAM(MT_, NT_, NC_)                                                          \
+  if (mt == MT_ && bn == NT_ * NC_)                                                       \
+    return launch_stream_u<MT_, NT_, NC_>(a, lda, b, ldb, e, W, ks, st);
+  I8L_STREAM(1, 1, 16) I8L_STREAM(2, 1, 16) I8L_STREAM(4, 1, 16) I8L_STREAM(8, 1, 16)
+  I8L_STREAM(1, 2, 16) I8L_STREAM(2, 2, 16) I8L_STREAM(4, 2, 16)
+  I8L_STREAM(1, 1, 8) I8L_STREAM(2, 1, 8) I8L_STREAM(1, 1, 4)
 #undef I8L_STREAM
   return hipErrorInvalidValue;
 }
@@ -596,8 +652,9 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
   const int osz = elt_size(out_dtype);
   const bool fast = K > 0 && stride_ak == 1 && stride_bk == 1 && aligned16(a) && aligned16(b) &&
                     stride_am % 16 == 0 && stride_bn % 16 == 0 && aligned16(out) &&
-                    (stride_cm * osz) % 16 == 0 && stride_cm >= N && N % 16 == 0 &&
-                    (e.sb_per_col == 0 || aligned16(scale_b));
+                    (stride_cm * osz) % 16 == 0 && stride_cm >= N && N % 4 == 0 &&
+                    (e.sb_per_col == 0 || aligned16(scale_b)) &&
+                    (e.bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
   hipError_t err;
   if (!fast) {
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));

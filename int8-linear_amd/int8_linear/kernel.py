@@ -82,10 +82,22 @@ def _tuned_table(device_name: str) -> dict:
     return tables.get(device_name, {})
 
 
+@lru_cache(maxsize=None)
+def _device_table(device: int) -> dict:
+    """The tuned table of this device: by marketing name as the reference keys it, else by
+    the architecture name (gfx950), which is what some ROCm installs report instead of the
+    product name."""
+    table = _tuned_table(torch.cuda.get_device_name(device))
+    if not table:
+        arch = getattr(torch.cuda.get_device_properties(device), "gcnArchName", "")
+        table = _tuned_table(arch.split(":")[0])
+    return table
+
+
 def tuned_config(m: int, n: int, k: int) -> Config | None:
     """The fastest measured config for this GPU and shape, from the largest tuned batch
     bucket at or below M, or None if nothing has been tuned (reference kernel.py:143-148)."""
-    table = _tuned_table(torch.cuda.get_device_name()).get(f"{k}x{n}", {})
+    table = _device_table(torch.cuda.current_device()).get(f"{k}x{n}", {})
     fits = [int(bucket) for bucket in table if int(bucket) <= m]
     return Config(**table[str(max(fits))]["config"]) if fits else None
 

@@ -93,8 +93,8 @@ def test_tuned_config_takes_the_largest_bucket_at_or_below_m(monkeypatch):
                                            "stages": 1, "group_m": 1}},
                            "17": {"config": {"bm": 32, "bn": 16, "bk": 512, "warps": 8,
                                             "stages": 1, "group_m": 1}}}}
-    monkeypatch.setattr(kernel.torch.cuda, "get_device_name", lambda *a: "TEST GPU")
-    monkeypatch.setattr(kernel, "_tuned_table", lambda name: table if name == "TEST GPU" else {})
+    monkeypatch.setattr(kernel.torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(kernel, "_device_table", lambda dev: table)
     assert kernel.tuned_config(1, 4096, 2048).bm == 16
     assert kernel.tuned_config(16, 4096, 2048).bm == 16
     assert kernel.tuned_config(17, 4096, 2048).bm == 32

@@ -58,6 +58,7 @@ def test_int32_product_is_exact(m, k, n):
 
 TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64, 16, 512, 8, 1, 1),
            Config(128, 16, 256, 4, 1, 1), Config(16, 32, 512, 8, 1, 1),
+           Config(16, 8, 256, 4, 1, 1), Config(32, 8, 512, 8, 1, 1), Config(16, 4, 128, 2, 1, 1),
            Config(128, 128, 64, 4, 2, 8), Config(256, 128, 64, 4, 2, 1),
            Config(128, 256, 64, 4, 2, 1), Config(256, 256, 64, 4, 2, 8),
            Config(256, 256, 128, 4, 2, 8), Config(128, 128, 128, 4, 2, 1)]
