@@ -30,8 +30,17 @@ ROTATE_BYTES = 512 << 20
 # (MT, bn) of the built weight-streaming tiles: bm = 16*MT tokens, bn output columns
 STREAM_TILES = [(1, 16), (2, 16), (4, 16), (8, 16), (1, 32), (2, 32), (4, 32), (1, 8), (2, 8),
                 (1, 4)]
-STAGED_TILES = [(128, 128, 64), (256, 128, 64), (128, 256, 64), (256, 256, 64),
-                (256, 256, 128), (128, 128, 128)]
+# (BM, BN, BK, waves) of the built staged tiles
+STAGED_TILES = [(128, 128, 64, 4), (256, 128, 64, 4), (128, 256, 64, 4), (256, 256, 64, 4),
+                (256, 256, 128, 4), (128, 128, 128, 4), (256, 256, 64, 8), (256, 256, 128, 8),
+                (256, 128, 64, 8), (128, 256, 64, 8), (256, 128, 128, 8), (128, 256, 128, 8)]
+
+
+# (BM, BN, BK, waves, ring depth) of the built direct-to-LDS tiles
+DMA_TILES = [(256, 256, 64, 4, 3), (256, 256, 64, 4, 4), (256, 256, 64, 8, 3),
+             (256, 256, 64, 8, 4), (256, 128, 64, 8, 4), (128, 256, 64, 8, 4),
+             (256, 128, 128, 8, 3), (128, 256, 128, 8, 3), (128, 128, 128, 4, 4),
+             (128, 128, 64, 4, 4)]
 
 
 def candidate_configs(m: int, k: int, n: int) -> list[Config]:
@@ -47,9 +56,14 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
                 if supported(m, n, k, cfg):
                     out.append(cfg)
     if m >= 64:
-        for bm, bn, bk in STAGED_TILES:
+        for bm, bn, bk, w in STAGED_TILES:
             for g in (1, 8):
-                cfg = Config(bm, bn, bk, 4, 2, g)
+                cfg = Config(bm, bn, bk, w, 2, g)
+                if supported(m, n, k, cfg):
+                    out.append(cfg)
+        for bm, bn, bk, w, st in DMA_TILES:
+            for g in (1, 8):
+                cfg = Config(bm, bn, bk, w, st, g)
                 if supported(m, n, k, cfg):
                     out.append(cfg)
     return out

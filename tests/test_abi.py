@@ -45,8 +45,10 @@ def test_default_config_regimes():
     assert default_config(17, 4096, 2048).bm == 32          # one tile covers M=17
     assert default_config(128, 2048, 6144).bm == 128
     p = default_config(4096, 28672, 4096)
-    assert p.stages == 2 and (p.bm, p.bn) == (256, 256)
-    assert default_config(300, 2048, 2048).stages == 2
+    assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
+    assert default_config(300, 2048, 2048).stages >= 2
+    for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
+        assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
 
 
 def test_supported_decline_rule_matches_reference():
@@ -56,7 +58,8 @@ def test_supported_decline_rule_matches_reference():
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 3, 1))  # 3 stages: not built
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 4, 2, 8))
-    assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 2, 8))
+    assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 4, 8))   # DMA ring of 4
+    assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 16, 2, 8))
 
 
 def test_supported_reports_the_reason():

@@ -61,7 +61,12 @@ TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64,
            Config(16, 8, 256, 4, 1, 1), Config(32, 8, 512, 8, 1, 1), Config(16, 4, 128, 2, 1, 1),
            Config(128, 128, 64, 4, 2, 8), Config(256, 128, 64, 4, 2, 1),
            Config(128, 256, 64, 4, 2, 1), Config(256, 256, 64, 4, 2, 8),
-           Config(256, 256, 128, 4, 2, 8), Config(128, 128, 128, 4, 2, 1)]
+           Config(256, 256, 128, 4, 2, 8), Config(128, 128, 128, 4, 2, 1),
+           Config(256, 256, 64, 8, 2, 8), Config(256, 128, 64, 8, 2, 1),
+           Config(128, 256, 128, 8, 2, 8),
+           Config(256, 256, 64, 4, 3, 8), Config(256, 256, 64, 8, 4, 8),
+           Config(256, 128, 64, 8, 4, 1), Config(128, 256, 128, 8, 3, 8),
+           Config(128, 128, 64, 4, 4, 1)]
 
 
 @pytest.mark.parametrize("config", TILINGS, ids=lambda c: c.name.replace(" ", "_"))
