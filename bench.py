@@ -131,6 +131,51 @@ class Sweep:
                        d["bias"])
 
 
+TRAFFIC_PATH = ROOT / "profiles" / "traffic_config0.json"
+
+
+def roofline_config0(dev, launches: int = 0) -> dict:
+    """Roofline object of the dominant kernel: the decode GEMM at BASELINE config 0 (qkv_proj,
+    M=16, K=2048, N=4096, no bias, bf16 out), weights rotating through >= 768 MiB of copies.
+    `achieved` = algorithmic bytes per launch / average launch time of back-to-back launches
+    in a HIP graph, timed with HIP events on the stream the graph is launched on."""
+    import torch
+
+    from int8_linear import w8a8_mm
+    from int8_linear.kernel import choose_config
+    from int8_linear.operands import operands, seed_of
+    m, k, n = 16, 2048, 4096
+    d = operands(m, k, n, seed_of(m, k, n), device=dev)
+    copies = max(2, -(-ROTATE_BYTES // (k * n)))
+    ws = [d["w_q"]] + [d["w_q"].clone() for _ in range(copies - 1)]
+    cfg = choose_config(m, n, k)
+    reps = launches or 2 * copies
+    us = graph_time_us(lambda i: w8a8_mm(d["a_q"], ws[i % copies].t(), d["a_s"], d["w_s"],
+                                         torch.bfloat16), reps)
+    b0 = gemm_bytes(m, k, n, False)
+    ach = b0 / (us * 1e-6) / 1e9
+    traffic = None
+    if TRAFFIC_PATH.exists():
+        rec = json.loads(TRAFFIC_PATH.read_text())
+        if rec.get("config") == cfg.name:
+            traffic = rec["bytes_per_launch"]
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": f"gemm_stream, config {cfg.name} (BASELINE config 0: M=16 K=2048 N=4096)",
+            "bytes_per_launch": b0, "avg_launch_us": round(us, 3), "launches": reps}
+
+
+def copy_calibration(dev, mib: int = 256) -> dict:
+    """A plain device copy of known size (for scaling FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes": mib << 20, "copies": 3}
+
+
 def cpu_baseline() -> dict:
     """The oracle's CPU restatement of the reference's path (exact int32 product + fp32
     dequant + bf16 cast) on the config-0 shape, repeated for about 10 s."""
@@ -162,6 +207,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 2-3 and per-point table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the config-0 roofline launches (and a copy of known size), for "
+                         "rocprofv3 kernel-trace and counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
@@ -175,6 +223,11 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log("library:", _lib.lib().i8l_version().decode(), "device:", torch.cuda.get_device_name())
+    if args.roofline_only:
+        rf = roofline_config0(dev)
+        cal = copy_calibration(dev)
+        print(json.dumps({"roofline": rf, "calibration": cal}), flush=True)
+        return 0
     shapes = SHAPES["qwen3-1.7b-vllm"]
     sw = Sweep(shapes, DECODE_M, dev)
     log(f"sweep: {len(sw.points)} linears, {sw.copies} weight copies")
@@ -235,17 +288,9 @@ def main() -> int:
                    "sweep_GBps": round(sweep_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
     }
 
-    # roofline of the dominant kernel: the decode GEMM at config 0 (qkv, M=16), cold weights
-    qkv_idx = [i for i, p in enumerate(sw.points) if p[0] == "qkv_proj" and p[1] == 16 and not p[4]][0]
-    reps = 4 * sw.copies
-    us0 = graph_time_us(lambda i: sw.call(qkv_idx, i), reps)
-    b0 = gemm_bytes(16, 2048, 4096, False)
-    ach = b0 / (us0 * 1e-6) / 1e9
-    result["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                          "kernel": "gemm_stream (config 0: M=16 K=2048 N=4096)",
-                          "bytes_per_launch": b0, "avg_launch_us": round(us0, 3)}
-    log(f"roofline config0: {us0:.2f} us, {ach:.0f} GB/s ({ach / HBM_PEAK_GBS:.1%})")
+    result["roofline"] = roofline_config0(dev)
+    log(f"roofline config0: {result['roofline']['avg_launch_us']:.2f} us, "
+        f"{result['roofline']['achieved']:.0f} GB/s ({result['roofline']['frac']:.1%})")
 
     if not args.no_extra:
         table = []
