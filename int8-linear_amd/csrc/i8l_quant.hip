@@ -1,5 +1,5 @@
 // Fused per-token int8 quantizers for MI355X (gfx950): add+RMSNorm+quantize,
-// SiLU-and-mul+quantize and the plain per-token quantizer.  One workgroup per token row.
+// SiLU-and-mul+quantize and the plain per-token quantizer.
 //
 // Arithmetic follows the reference's Triton kernels step for step
 // (AshrithaG/int8-linear, int8_linear/fused_quant.py): the residual add and the norm in
@@ -11,91 +11,199 @@
 // Three points the reference leaves to Triton/libdevice are fixed here so that the CPU
 // oracle reproduces every bit:
 //   * sum(x^2) is a pairwise tree in double over the row padded with zeros to a power of
-//     two, leaf i = x_i^2 (exact in double); thread t owns the contiguous leaves
-//     [E*t, E*t+E), wave lanes combine by xor-butterfly and waves in pairwise order, which
-//     is the same perfect binary tree for every launch shape;  var = f32(sum / H);
+//     two, leaf i = x_i^2 (exact in double);  var = f32(sum / H);
 //   * rsqrt(v) = f32(1 / sqrt(double(v))) (IEEE double sqrt and divide);
 //   * exp is canon_expf (Cody-Waite + degree-7 Taylor with explicit fma).
 // Compiled with -ffp-contract=off: every other operation is the single IEEE fp32 op written.
+//
+// Launch layout.  A token row is owned by NW waves (NW = 1 for rows up to 2048 elements),
+// and a workgroup holds RPB rows.  The row is cut into 8-element chunks; lane l of wave w
+// owns chunks (w*J + j)*64 + l for j < J, so each load instruction of a wave reads 64
+// consecutive chunks (1 KiB of bf16) and each lane's chunk j is an aligned 8-leaf subtree.
+// The sum of squares is then evaluated as the perfect binary tree over the padded row:
+// the 8 leaves of a chunk in-lane, 64 chunks by a lane butterfly (DPP within 16-lane rows,
+// a swizzle across rows, a readlane across the halves) into an aligned 512-element node,
+// the J nodes of a wave pairwise, and the NW waves pairwise through LDS.  IEEE addition is
+// commutative, so both partners of each butterfly step hold the same node.  Maxima are
+// order-free.  A row owned by one wave needs no LDS and no barrier.
 #include "i8l_common.h"
 
 namespace i8l {
 
 namespace {
 
-__device__ __forceinline__ void unpack8(uint4 v, int dtype, float* o) {
+constexpr int kMaxWaves = 16;  // waves per workgroup (1024 threads)
+
+// ------------------------------------------------------------------ cross-lane moves
+// DPP controls (gfx9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
+constexpr int kQuadSwap1 = 0xB1, kQuadSwap2 = 0x4E, kHalfMirror = 0x141, kRowMirror = 0x140;
+// ds_swizzle bitmask mode: lane ^ 16 within each 32-lane half.
+constexpr int kSwizzleXor16 = 0x401F;
+
+// Every control used is a full permutation, so no lane reads an invalid source.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = dpp_i<CTRL>((int)(uint32_t)u), hi = dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+__device__ __forceinline__ double swz16_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)u, kSwizzleXor16);
+  const int hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), kSwizzleXor16);
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const int hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+
+// Sum over the 64 lanes as a perfect binary tree (lane i is leaf i); every lane returns it.
+__device__ __forceinline__ double wave_tree_sum(double v) {
+  v = v + dpp_d<kQuadSwap1>(v);    // pairs
+  v = v + dpp_d<kQuadSwap2>(v);    // quads
+  v = v + dpp_d<kHalfMirror>(v);   // 8 lanes: each quad is uniform, so mirroring pairs quads
+  v = v + dpp_d<kRowMirror>(v);    // 16 lanes
+  v = v + swz16_d(v);              // 32 lanes
+  return readlane_d(v, 0) + readlane_d(v, 32);
+}
+
+__device__ __forceinline__ float fmax_dpp1(float v) {
+  return fmaxf(v, __int_as_float(dpp_i<kQuadSwap1>(__float_as_int(v))));
+}
+// Maximum over the 64 lanes; every lane returns it.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmax_dpp1(v);
+  v = fmaxf(v, __int_as_float(dpp_i<kQuadSwap2>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<kHalfMirror>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<kRowMirror>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwizzleXor16)));
+  return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+}
+
+// ------------------------------------------------------------------ row chunks
+// Row geometry of one wave: which row, which of its NW waves, and the first element of
+// each of its J chunks.
+struct RowPos {
+  int64_t row;
+  int rw;     // wave index within the row
+  int slot;   // row index within the workgroup
+  int lane;
+};
+
+__device__ __forceinline__ RowPos row_pos(int nw, int rpb) {
+  RowPos p;
+  const int wave = threadIdx.x >> 6;
+  p.lane = threadIdx.x & 63;
+  p.rw = wave % nw;
+  p.slot = wave / nw;
+  p.row = (int64_t)blockIdx.x * rpb + p.slot;
+  return p;
+}
+
+template <int J>
+__device__ __forceinline__ int chunk_base(const RowPos& p, int j) {
+  return ((p.rw * J + j) * 64 + p.lane) * 8;
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(uint4 v, float* o) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    o[2 * i] = act_to_f32(w[i] & 0xffffu, dtype);
-    o[2 * i + 1] = act_to_f32(w[i] >> 16, dtype);
+    o[2 * i] = act_to_f32<DT>(w[i] & 0xffffu);
+    o[2 * i + 1] = act_to_f32<DT>(w[i] >> 16);
   }
 }
 
-// Load E consecutive elements [base, base+E) of a row of length n (zeros past the end).
-template <int E>
-__device__ __forceinline__ void load_row(const uint16_t* p, int base, int n, int dtype, bool vec,
-                                         float* o) {
-  if (vec) {
+// Elements [e0, e0+8) of a row of length n as floats (zeros past the end).  VEC: n is a
+// multiple of 8 and the row is 16-byte aligned, so a chunk is all in or all out.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(const uint16_t* p, int e0, int n, float* o) {
+  if (VEC) {
+    if (e0 < n) {
+      unpack8<DT>(*(const uint4*)(p + e0), o);
+    } else {
 #pragma unroll
-    for (int j = 0; j < E; j += 8) {
-      if (base + j < n) {
-        unpack8(*(const uint4*)(p + base + j), dtype, o + j);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[j + i] = 0.0f;
-      }
+      for (int i = 0; i < 8; ++i) o[i] = 0.0f;
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < E; ++j) o[j] = base + j < n ? act_to_f32(p[base + j], dtype) : 0.0f;
+    for (int i = 0; i < 8; ++i) o[i] = e0 + i < n ? act_to_f32<DT>(p[e0 + i]) : 0.0f;
   }
 }
 
-template <int E>
-__device__ __forceinline__ void store_act(uint16_t* p, int base, int n, int dtype, bool vec,
-                                          const float* v) {
-  if (vec) {
+// The 16-bit elements [e0, e0+8) of a row packed as they lie in memory (zeros past the end).
+template <bool VEC>
+__device__ __forceinline__ uint4 load_raw8(const uint16_t* p, int e0, int n) {
+  if (VEC) return e0 < n ? *(const uint4*)(p + e0) : make_uint4(0, 0, 0, 0);
+  uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < E; j += 8) {
-      if (base + j < n) {
-        uint32_t w[4];
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = e0 + 2 * i < n ? p[e0 + 2 * i] : 0u;
+    const uint32_t hi = e0 + 2 * i + 1 < n ? p[e0 + 2 * i + 1] : 0u;
+    w[i] = lo | (hi << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// Elements 2i and 2i+1 of a packed chunk as floats.
+template <int DT>
+__device__ __forceinline__ void unpack_pair(const uint4& v, int i, float& a, float& b) {
+  const uint32_t w = i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+  if (DT == I8L_BF16) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  } else {
+    a = act_to_f32<DT>(w & 0xffffu);
+    b = act_to_f32<DT>(w >> 16);
+  }
+}
+
+template <int DT, bool VEC>
+__device__ __forceinline__ void store8(uint16_t* p, int e0, int n, const float* v) {
+  if (VEC) {
+    if (e0 < n) {
+      uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          w[i] = f32_to_act(v[j + 2 * i], dtype) | ((uint32_t)f32_to_act(v[j + 2 * i + 1], dtype) << 16);
-        *(uint4*)(p + base + j) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
+      for (int i = 0; i < 4; ++i) w[i] = f32x2_to_act2<DT>(v[2 * i], v[2 * i + 1]);
+      *(uint4*)(p + e0) = make_uint4(w[0], w[1], w[2], w[3]);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < E; ++j)
-      if (base + j < n) p[base + j] = f32_to_act(v[j], dtype);
+    for (int i = 0; i < 8; ++i)
+      if (e0 + i < n) p[e0 + i] = f32_to_act<DT>(v[i]);
   }
 }
 
-// Block-wide max of non-negative floats (exact: max is order-free).
-__device__ __forceinline__ float block_max(float v, float* sh) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6;
+// Max of non-negative values over the NW waves of a row: each wave's maximum goes through
+// LDS (sh holds kMaxWaves floats) and comes back as lanes 0..nw-1 of every wave of the row.
+__device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float* sh) {
+  v = wave_max(v);
   if (nw == 1) return v;
-  __syncthreads();  // sh may still be read by a previous reduction
-  if ((threadIdx.x & 63) == 0) sh[wave] = v;
+  if (p.lane == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
-  float m = sh[0];
-  for (int w = 1; w < nw; ++w) m = fmaxf(m, sh[w]);
-  return m;
+  return wave_max(p.lane < nw ? sh[p.slot * nw + p.lane] : 0.0f);
 }
 
-// Quantize E values of one row and store the codes; thread 0 stores the scale.
-template <int E>
-__device__ __forceinline__ void quantize_store(const float* y, int base, int n, int8_t* qrow,
-                                               float* scale_out, bool vec, int precise,
+// The quantizer of a row whose values y (J chunks of 8 per lane) are final: absmax over the
+// row, scale and reciprocal, codes stored as 8-byte pieces, the scale by the row's first lane.
+template <int J, bool VEC>
+__device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p, int n, int nw,
+                                               int8_t* qrow, float* scale_out, int precise,
                                                float* sh) {
   float am = 0.0f;
 #pragma unroll
-  for (int j = 0; j < E; ++j) am = fmaxf(am, fabsf(y[j]));
-  const float absmax = block_max(am, sh);
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(y[j][i]));
+  const float absmax = row_max(am, p, nw, sh);
   float scale, inv;
   if (precise) {
     scale = absmax / 127.0f;
@@ -104,120 +212,191 @@ __device__ __forceinline__ void quantize_store(const float* y, int base, int n, 
     scale = absmax * (1.0f / 127.0f);
     inv = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
   }
-  if (threadIdx.x == 0) *scale_out = scale;
-  int8_t c[E];
+  if (p.rw == 0 && p.lane == 0) *scale_out = scale;
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    float v = __builtin_rintf(y[j] * inv);
-    v = fminf(fmaxf(v, -128.0f), 127.0f);
-    c[j] = (int8_t)(int)v;
-  }
-  if (vec) {
+  for (int j = 0; j < J; ++j) {
+    const int e0 = chunk_base<J>(p, j);
+    uint32_t c[8];
 #pragma unroll
-    for (int j = 0; j < E; j += 8) {
-      if (base + j < n) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lo |= (uint32_t)(uint8_t)c[j + i] << (8 * i);
-          hi |= (uint32_t)(uint8_t)c[j + 4 + i] << (8 * i);
-        }
-        *(uint2*)(qrow + base + j) = make_uint2(lo, hi);
-      }
+    for (int i = 0; i < 8; ++i) {
+      float v = __builtin_rintf(y[j][i] * inv);
+      v = fminf(fmaxf(v, -128.0f), 127.0f);
+      c[i] = (uint32_t)(int)v & 0xffu;
     }
-  } else {
+    if (VEC) {
+      if (e0 < n) {
+        const uint32_t lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        const uint32_t hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        *(uint2*)(qrow + e0) = make_uint2(lo, hi);
+      }
+    } else {
 #pragma unroll
-    for (int j = 0; j < E; ++j)
-      if (base + j < n) qrow[base + j] = c[j];
+      for (int i = 0; i < 8; ++i)
+        if (e0 + i < n) qrow[e0 + i] = (int8_t)c[i];
+    }
   }
 }
 
 // ------------------------------------------------------------------ add + RMSNorm + quant
-template <int E>
+// J and NW are powers of two, so each wave covers an aligned power-of-two span of the row
+// and the wave/chunk/lane reductions together evaluate the padded row's pairwise tree.
+template <int J, int DT, int WDT, bool VEC>
 __global__ void __launch_bounds__(1024)
 add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
                          const uint16_t* __restrict__ w, float eps, int8_t* __restrict__ q,
-                         float* __restrict__ scale, uint16_t* __restrict__ rout, int H, int act,
-                         int wdt, int precise, int vec) {
-  __shared__ double dsh[16];
-  __shared__ float fsh[16];
-  const int64_t row = blockIdx.x;
-  const int base = threadIdx.x * E;
-  float xv[E];
-  load_row<E>(x + row * H, base, H, act, vec, xv);
+                         float* __restrict__ scale, uint16_t* __restrict__ rout, int64_t M,
+                         int H, int nw, int rpb, int precise) {
+  __shared__ double dsh[kMaxWaves];
+  __shared__ float fsh[kMaxWaves];
+  const RowPos p = row_pos(nw, rpb);
+  if (p.row >= M) return;  // whole single-wave rows only: a row of nw > 1 waves has rpb = 1
+  const int64_t ro = p.row * H;
+  float xv[J][8];
+#pragma unroll
+  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + ro, chunk_base<J>(p, j), H, xv[j]);
   if (res) {
-    float rv[E];
-    load_row<E>(res + row * H, base, H, act, vec, rv);
+    float rv[J][8];
 #pragma unroll
-    for (int j = 0; j < E; ++j) xv[j] = xv[j] + rv[j];
-    store_act<E>(rout + row * H, base, H, act, vec, xv);
+    for (int j = 0; j < J; ++j) load8<DT, VEC>(res + ro, chunk_base<J>(p, j), H, rv[j]);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[j][i] = xv[j][i] + rv[j][i];
+      store8<DT, VEC>(rout + ro, chunk_base<J>(p, j), H, xv[j]);
+    }
   }
-  // pairwise tree of x^2 in double: thread-local subtree, then lanes, then waves
-  double s[E];
+  // sum of squares: leaves in-lane, then lanes, then the wave's chunks, then waves
+  double node[J];
 #pragma unroll
-  for (int j = 0; j < E; ++j) s[j] = (double)xv[j] * (double)xv[j];
+  for (int j = 0; j < J; ++j) {
+    double s[8];
 #pragma unroll
-  for (int st = 1; st < E; st <<= 1)
+    for (int i = 0; i < 8; ++i) s[i] = (double)xv[j][i] * (double)xv[j][i];
 #pragma unroll
-    for (int j = 0; j < E; j += 2 * st) s[j] = s[j] + s[j + st];
-  double tot = s[0];
+    for (int st = 1; st < 8; st <<= 1)
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) tot = tot + __shfl_xor(tot, o);
-  const int nw = blockDim.x >> 6;
+      for (int i = 0; i < 8; i += 2 * st) s[i] = s[i] + s[i + st];
+    node[j] = wave_tree_sum(s[0]);
+  }
+#pragma unroll
+  for (int st = 1; st < J; st <<= 1)
+#pragma unroll
+    for (int j = 0; j < J; j += 2 * st) node[j] = node[j] + node[j + st];
+  double tot = node[0];
   if (nw > 1) {
-    if ((threadIdx.x & 63) == 0) dsh[threadIdx.x >> 6] = tot;
+    // the nw wave nodes (aligned, a power of two of them) become lanes 0..nw-1 of a tree
+    // whose other leaves are +0, which leaves every sum unchanged
+    if (p.lane == 0) dsh[threadIdx.x >> 6] = tot;
     __syncthreads();
-    double v[16];
-    for (int i = 0; i < nw; ++i) v[i] = dsh[i];
-    for (int st = 1; st < nw; st <<= 1)
-      for (int i = 0; i < nw; i += 2 * st) v[i] = v[i] + v[i + st];
-    tot = v[0];
+    tot = wave_tree_sum(p.lane < nw ? dsh[p.slot * nw + p.lane] : 0.0);
   }
   const float var = (float)(tot / (double)H);
   const float rs = canon_rsqrtf(var + eps);
-  float wv[E];
-  load_row<E>(w, base, H, wdt, vec, wv);
-  float y[E];
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    const float xn = xv[j] * rs;
-    y[j] = round_through(round_through(xn, wdt) * wv[j], act);
+  for (int j = 0; j < J; ++j) {
+    float wv[8];
+    load8<WDT, VEC>(w, chunk_base<J>(p, j), H, wv);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      float a = xv[j][i] * rs, b = xv[j][i + 1] * rs;
+      round_through2<WDT>(a, b);
+      a = a * wv[i];
+      b = b * wv[i + 1];
+      round_through2<DT>(a, b);
+      xv[j][i] = a;
+      xv[j][i + 1] = b;
+    }
   }
-  quantize_store<E>(y, base, H, q + row * H, scale + row, vec, precise, fsh);
+  quantize_store<J, VEC>(xv, p, H, nw, q + ro, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ SiLU-and-mul + quant
-template <int E>
+template <int J, int DT, bool VEC, bool ROUND>
 __global__ void __launch_bounds__(1024)
 silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
-                      float* __restrict__ scale, int I, int act, int round_silu, int precise,
-                      int vec) {
-  __shared__ float fsh[16];
-  const int64_t row = blockIdx.x;
-  const int base = threadIdx.x * E;
-  float g[E], u[E], y[E];
-  load_row<E>(gu + row * 2 * I, base, I, act, vec, g);
-  load_row<E>(gu + row * 2 * I + I, base, I, act, vec, u);
+                      float* __restrict__ scale, int64_t M, int I, int nw, int rpb,
+                      int precise) {
+  __shared__ float fsh[kMaxWaves];
+  const RowPos p = row_pos(nw, rpb);
+  if (p.row >= M) return;
+  const uint16_t* grow = gu + p.row * 2 * I;
+  uint4 graw[J], uraw[J];
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    float a = g[j] / (1.0f + canon_expf(-g[j]));
-    if (round_silu) a = round_through(a, act);
-    y[j] = round_through(a * u[j], act);
+  for (int j = 0; j < J; ++j) {
+    graw[j] = load_raw8<VEC>(grow, chunk_base<J>(p, j), I);
+    uraw[j] = load_raw8<VEC>(grow + I, chunk_base<J>(p, j), I);
   }
-  quantize_store<E>(y, base, I, q + row * I, scale + row, vec, precise, fsh);
+  // d = 1 + exp(-g).  The range selects of canon_expf do not change d: below the normal
+  // range exp is < 2^-24 and 1 + e rounds to 1 either way, the clamp already overflows
+  // to +inf above 89, and a NaN g makes the quotient NaN whatever d is (checked for every
+  // bf16 and fp16 g on gfx950).
+  // a = g / d.  For -87 < g < +inf, d is in [1, 7e37], its reciprocal is normal, and one
+  // Newton-Markstein correction of g * rcp(d) gives the correctly rounded quotient, with the
+  // sign copied from g so that g = -0 gives -0 (checked against IEEE division for every
+  // bf16 and fp16 g in that range on gfx950).  A wave holding any other g recomputes its
+  // values with IEEE division.
+  float y[J][8];
+  float gmin = __builtin_inff(), gmax = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float g[2], u[2], a[2];
+      unpack_pair<DT>(graw[j], i, g[0], g[1]);
+      unpack_pair<DT>(uraw[j], i, u[0], u[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float d = 1.0f + canon_expf_core(__builtin_amdgcn_fmed3f(-g[h], -87.5f, 89.5f));
+        const float r0 = __builtin_amdgcn_rcpf(d);
+        const float q0 = g[h] * r0;
+        const float e = __builtin_fmaf(-d, q0, g[h]);
+        const float q1 = __builtin_fmaf(e, r0, q0);
+        a[h] = __uint_as_float((__float_as_uint(q1) & 0x7fffffffu) |
+                               (__float_as_uint(g[h]) & 0x80000000u));
+        gmin = fminf(gmin, g[h]);
+        gmax = fmaxf(gmax, g[h]);
+      }
+      if (ROUND) round_through2<DT>(a[0], a[1]);
+      a[0] = a[0] * u[0];
+      a[1] = a[1] * u[1];
+      round_through2<DT>(a[0], a[1]);
+      y[j][2 * i] = a[0];
+      y[j][2 * i + 1] = a[1];
+    }
+  if (!__all(gmin > -87.0f && gmax < __builtin_inff())) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g[2], u[2], a[2];
+        unpack_pair<DT>(graw[j], i, g[0], g[1]);
+        unpack_pair<DT>(uraw[j], i, u[0], u[1]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          a[h] = g[h] / (1.0f + canon_expf_core(__builtin_amdgcn_fmed3f(-g[h], -87.5f, 89.5f)));
+        if (ROUND) round_through2<DT>(a[0], a[1]);
+        a[0] = a[0] * u[0];
+        a[1] = a[1] * u[1];
+        round_through2<DT>(a[0], a[1]);
+        y[j][2 * i] = a[0];
+        y[j][2 * i + 1] = a[1];
+      }
+  }
+  quantize_store<J, VEC>(y, p, I, nw, q + p.row * I, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ plain per-token quant
-template <int E>
+template <int J, int DT, bool VEC>
 __global__ void __launch_bounds__(1024)
 quant_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scale,
-             int H, int act, int precise, int vec) {
-  __shared__ float fsh[16];
-  const int64_t row = blockIdx.x;
-  const int base = threadIdx.x * E;
-  float y[E];
-  load_row<E>(x + row * H, base, H, act, vec, y);
-  quantize_store<E>(y, base, H, q + row * H, scale + row, vec, precise, fsh);
+             int64_t M, int H, int nw, int rpb, int precise) {
+  __shared__ float fsh[kMaxWaves];
+  const RowPos p = row_pos(nw, rpb);
+  if (p.row >= M) return;
+  float y[J][8];
+#pragma unroll
+  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + p.row * H, chunk_base<J>(p, j), H, y[j]);
+  quantize_store<J, VEC>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -230,23 +409,102 @@ int next_pow2(int v) {
 
 bool act_ok(int dt) { return dt == I8L_BF16 || dt == I8L_F16; }
 
-// elements per thread: 8 up to 8192 elements a row, then 16, 32
-int pick_e(int n) { return n <= 8192 ? 8 : n <= 16384 ? 16 : 32; }
+// Launch geometry: J chunks per lane, NW waves per row, RPB rows per workgroup.  A workgroup
+// holds several rows only when each row is one wave: such rows never meet at a barrier, so a
+// wave whose row is past M may return early.
+struct Geom {
+  int j, nw, rpb;
+};
+
+// Up to this many waves in total, a row is spread over as many waves as possible (one chunk
+// a lane): a few rows are latency-bound, and more waves shorten each lane's serial work.
+// Beyond it, each wave takes up to 4 chunks a lane, which keeps more bytes in flight per
+// wave and reduces cross-wave reductions.
+constexpr int64_t kSpreadWaves = 4096;
+
+// RMSNorm: powers of two throughout (the sum tree needs aligned power-of-two spans).
+Geom norm_geom(int64_t M, int h, bool vec) {
+  const int p = next_pow2(h);
+  Geom g;
+  const int64_t spread = (int64_t)M * ((p + 511) / 512);
+  if (vec && spread <= kSpreadWaves) {
+    g.nw = p / 512 < 1 ? 1 : p / 512;
+    g.j = 1;
+    while (g.nw > kMaxWaves) g.nw /= 2, g.j *= 2;
+  } else {
+    g.j = !vec ? 4 : p <= 512 ? 1 : p <= 1024 ? 2 : 4;
+    g.nw = p / (512 * g.j) < 1 ? 1 : p / (512 * g.j);
+  }
+  g.rpb = g.nw == 1 ? 4 : 1;
+  return g;
+}
+
+// Max-only kernels: any split of the row works.
+Geom flat_geom(int64_t M, int n, bool vec) {
+  const int chunks = (n + 7) / 8;
+  Geom g;
+  const int spread_nw = (chunks + 63) / 64;
+  if (vec && spread_nw <= kMaxWaves && (int64_t)M * spread_nw <= kSpreadWaves) {
+    g.nw = spread_nw;
+    g.j = 1;
+  } else {
+    g.nw = (chunks + 255) / 256;
+    g.j = vec ? (chunks + 64 * g.nw - 1) / (64 * g.nw) : 4;
+  }
+  g.rpb = g.nw == 1 ? 4 : 1;
+  return g;
+}
+
+dim3 grid_of(int64_t M, const Geom& g) { return dim3((unsigned)((M + g.rpb - 1) / g.rpb)); }
+dim3 block_of(const Geom& g) { return dim3(64 * g.nw * g.rpb); }
+
+// Kernel selection: the element path (VEC false) is built for J = 4 only.
+template <int DT, int WDT>
+void launch_norm(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                 const uint16_t* res, const uint16_t* w, float eps, int8_t* q, float* scale,
+                 uint16_t* rout, int64_t M, int H, int precise) {
+#define I8L_NORM(J_, V_)                                                                    \
+  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<J_, DT, WDT, V_>), grid, block_of(g), 0, st, x, \
+                     res, w, eps, q, scale, rout, M, H, g.nw, g.rpb, precise)
+  if (!vec) I8L_NORM(4, false);
+  else if (g.j == 1) I8L_NORM(1, true);
+  else if (g.j == 2) I8L_NORM(2, true);
+  else I8L_NORM(4, true);
+#undef I8L_NORM
+}
+
+template <int DT, bool ROUND>
+void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* gu,
+                 int8_t* q, float* scale, int64_t M, int I, int precise) {
+#define I8L_SILU(J_, V_)                                                                    \
+  hipLaunchKernelGGL((silu_mul_quant_kernel<J_, DT, V_, ROUND>), grid, block_of(g), 0, st, gu, \
+                     q, scale, M, I, g.nw, g.rpb, precise)
+  if (!vec) I8L_SILU(4, false);
+  else if (g.j == 1) I8L_SILU(1, true);
+  else if (g.j == 2) I8L_SILU(2, true);
+  else if (g.j == 3) I8L_SILU(3, true);
+  else I8L_SILU(4, true);
+#undef I8L_SILU
+}
+
+template <int DT>
+void launch_quant(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                  int8_t* q, float* scale, int64_t M, int H, int precise) {
+#define I8L_QUANT(J_, V_)                                                                   \
+  hipLaunchKernelGGL((quant_kernel<J_, DT, V_>), grid, block_of(g), 0, st, x, q, scale, M, H, \
+                     g.nw, g.rpb, precise)
+  if (!vec) I8L_QUANT(4, false);
+  else if (g.j == 1) I8L_QUANT(1, true);
+  else if (g.j == 2) I8L_QUANT(2, true);
+  else if (g.j == 3) I8L_QUANT(3, true);
+  else I8L_QUANT(4, true);
+#undef I8L_QUANT
+}
 
 }  // namespace
 }  // namespace i8l
 
 using namespace i8l;
-
-#define I8L_DISPATCH_E(E_, KERNEL, GRID, BLOCK, STREAM, ...)                               \
-  do {                                                                                    \
-    if (E_ == 8)                                                                          \
-      hipLaunchKernelGGL(KERNEL<8>, GRID, BLOCK, 0, STREAM, __VA_ARGS__);                  \
-    else if (E_ == 16)                                                                    \
-      hipLaunchKernelGGL(KERNEL<16>, GRID, BLOCK, 0, STREAM, __VA_ARGS__);                 \
-    else                                                                                  \
-      hipLaunchKernelGGL(KERNEL<32>, GRID, BLOCK, 0, STREAM, __VA_ARGS__);                 \
-  } while (0)
 
 extern "C" int i8l_add_rmsnorm_quant(const void* x, const void* residual, const void* weight,
                                      float eps, int8_t* q, float* scale, void* residual_out,
@@ -269,12 +527,19 @@ extern "C" int i8l_add_rmsnorm_quant(const void* x, const void* residual, const 
     return I8L_UNSUPPORTED;
   }
   if (M == 0) return I8L_OK;
-  const int h = (int)H, P = next_pow2(h), E = pick_e(P);
-  const int T = P / E < 64 ? 64 : P / E;
-  const bool vec = h % 8 == 0 && a16(x) && a16(weight) && a16(q) && (!residual || (a16(residual) && a16(residual_out)));
-  I8L_DISPATCH_E(E, add_rmsnorm_quant_kernel, dim3((unsigned)M), dim3(T), (hipStream_t)stream,
-                 (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)weight, eps, q,
-                 scale, (uint16_t*)residual_out, h, act_dtype, w_dtype, precise_div, (int)vec);
+  const int h = (int)H;
+  const bool vec = h % 8 == 0 && a16(x) && a16(weight) && a16(q) &&
+                   (!residual || (a16(residual) && a16(residual_out)));
+  const Geom g = norm_geom(M, h, vec);
+  const hipStream_t st = (hipStream_t)stream;
+  auto go = [&](auto launch) {
+    launch(g, vec, grid_of(M, g), st, (const uint16_t*)x, (const uint16_t*)residual,
+           (const uint16_t*)weight, eps, q, scale, (uint16_t*)residual_out, M, h, precise_div);
+  };
+  if (act_dtype == I8L_BF16)
+    w_dtype == I8L_BF16 ? go(launch_norm<I8L_BF16, I8L_BF16>) : go(launch_norm<I8L_BF16, I8L_F16>);
+  else
+    w_dtype == I8L_BF16 ? go(launch_norm<I8L_F16, I8L_BF16>) : go(launch_norm<I8L_F16, I8L_F16>);
   return hip_status(hipGetLastError(), "add_rmsnorm_quant launch");
 }
 
@@ -294,13 +559,17 @@ extern "C" int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale, 
     return I8L_UNSUPPORTED;
   }
   if (M == 0) return I8L_OK;
-  const int i = (int)I, E = pick_e(i);
-  int T = (i + E - 1) / E;
-  T = (T + 63) / 64 * 64;
+  const int i = (int)I;
   const bool vec = i % 8 == 0 && a16(gate_up) && a16(q);
-  I8L_DISPATCH_E(E, silu_mul_quant_kernel, dim3((unsigned)M), dim3(T), (hipStream_t)stream,
-                 (const uint16_t*)gate_up, q, scale, i, act_dtype, round_silu, precise_div,
-                 (int)vec);
+  const Geom g = flat_geom(M, i, vec);
+  const hipStream_t st = (hipStream_t)stream;
+  auto go = [&](auto launch) {
+    launch(g, vec, grid_of(M, g), st, (const uint16_t*)gate_up, q, scale, M, i, precise_div);
+  };
+  if (act_dtype == I8L_BF16)
+    round_silu ? go(launch_silu<I8L_BF16, true>) : go(launch_silu<I8L_BF16, false>);
+  else
+    round_silu ? go(launch_silu<I8L_F16, true>) : go(launch_silu<I8L_F16, false>);
   return hip_status(hipGetLastError(), "silu_mul_quant launch");
 }
 
@@ -319,11 +588,13 @@ extern "C" int i8l_quant_per_token(const void* x, int8_t* q, float* scale, int64
     return I8L_UNSUPPORTED;
   }
   if (M == 0) return I8L_OK;
-  const int h = (int)H, E = pick_e(h);
-  int T = (h + E - 1) / E;
-  T = (T + 63) / 64 * 64;
+  const int h = (int)H;
   const bool vec = h % 8 == 0 && a16(x) && a16(q);
-  I8L_DISPATCH_E(E, quant_kernel, dim3((unsigned)M), dim3(T), (hipStream_t)stream,
-                 (const uint16_t*)x, q, scale, h, act_dtype, precise_div, (int)vec);
+  const Geom g = flat_geom(M, h, vec);
+  const hipStream_t st = (hipStream_t)stream;
+  if (act_dtype == I8L_BF16)
+    launch_quant<I8L_BF16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, q, scale, M, h, precise_div);
+  else
+    launch_quant<I8L_F16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, q, scale, M, h, precise_div);
   return hip_status(hipGetLastError(), "quant_per_token launch");
 }

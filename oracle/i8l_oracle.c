@@ -35,10 +35,13 @@
 static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 
-/* float -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (c10/util/BFloat16.h rule). */
+/* float -> bf16 bits, round to nearest even (torch's rule for every non-NaN value).  A NaN
+ * becomes the quiet NaN (u >> 16) | 0x40, keeping its sign and top payload bits: the rule
+ * of the gfx950 conversion instruction the device code uses (torch writes 0x7FC0 for every
+ * NaN, NVIDIA hardware 0x7FFF; no reference result depends on the payload). */
 uint16_t or_f32_to_bf16(float f) {
   uint32_t u = f2u(f);
-  if (f != f) return 0x7fc0;
+  if (f != f) return (uint16_t)((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }

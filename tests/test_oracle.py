@@ -147,8 +147,12 @@ def test_bf16_conversion_matches_torch():
     x = np.concatenate([x, ties[np.isfinite(ties)]])
     ref = bf16_to_bits(torch.from_numpy(x).to(torch.bfloat16))
     assert np.array_equal(o.f32_to_bf16(x), ref)
-    nan = o.f32_to_bf16(np.array([np.nan], np.float32))
-    assert nan[0] == 0x7FC0
+    # NaN: a quiet NaN with the input's sign and top payload bits (the gfx950 conversion's
+    # rule); torch's canonical NaN 0x7FC0 is the case of a payload-free positive NaN
+    nans = np.array([0x7FC00000, 0xFFC00001, 0x7F800001, 0xFF800001, 0x7FFFFFFF, 0x7FA51234],
+                    np.uint32).view(np.float32)
+    assert o.f32_to_bf16(nans).tolist() == [0x7FC0, 0xFFC0, 0x7FC0, 0xFFC0, 0x7FFF, 0x7FE5]
+    assert o.f32_to_bf16(np.array([np.nan], np.float32))[0] == 0x7FC0
 
 
 def test_f16_conversion_matches_torch():

@@ -75,8 +75,12 @@ def check_norm(x, r, w, precise=True):
     return q, s, rout
 
 
+# Beyond the reference's shapes, rows that exercise every launch geometry of the kernel:
+# one chunk a lane (100), two (520, 1001 unaligned), rows of 2, 4, 8 and 16 waves
+# (4096, 6144, 16384, 32768), and M not a multiple of the 4 rows a workgroup holds.
 @pytest.mark.parametrize("m,k", [(1, 2048), (7, 2048), (64, 1024), (300, 2048), (5, 1000),
-                                 (3, 13), (2, 6144)])
+                                 (3, 13), (2, 6144), (6, 100), (9, 520), (5, 1001), (5, 4096),
+                                 (2, 16384), (3, 32768)])
 @pytest.mark.parametrize("has_res", [False, True])
 def test_add_rmsnorm_quant(m, k, has_res):
     say(f"add_rmsnorm_quant m={m} k={k} res={has_res}")
@@ -118,13 +122,34 @@ def check_silu(gu, round_silu, precise=True):
     return q, s
 
 
-@pytest.mark.parametrize("m,i", [(1, 6144), (33, 6144), (8, 1000), (3, 13), (2, 12000)])
+@pytest.mark.parametrize("m,i", [(1, 6144), (33, 6144), (8, 1000), (3, 13), (2, 12000),
+                                 (5, 1536), (6, 2048), (2, 32768)])
 @pytest.mark.parametrize("round_silu", [False, True])
 def test_silu_mul_quant(m, i, round_silu):
     say(f"silu_mul_quant m={m} i={i} round={round_silu}")
     gu = randn((m, 2 * i), m, 2.0)
     q, s = check_silu(gu, round_silu)
     assert_close_int8(q, s, *ref_silu(gu, round_silu))
+
+
+@pytest.mark.parametrize("i", [64, 6144])
+def test_silu_mul_quant_extreme_gates(i):
+    """Gates of -0.0 and at or below -87 (where 1 + exp(-g) is huge or infinite) send their
+    wave to the IEEE-division path; the other rows of the same launch stay on the fast path."""
+    say(f"silu_mul_quant extreme gates i={i}")
+    m = 6
+    gu = randn((m, 2 * i), 80 + i, 2.0).cpu()
+    special = torch.tensor([-0.0, -87.0, -87.5, -88.0, -89.0, -100.0, -1e30, -3e38, 0.0, 87.5],
+                           dtype=torch.bfloat16)
+    gu[1, :special.numel()] = special                      # row 1: extreme gates
+    gu[3, i - 3:i] = special[:3]                           # row 3: at the end of the gate half
+    gu[4, :i] = -0.0                                       # row 4: all gates -0.0
+    gu = gu.cuda()
+    for rs in (False, True):
+        q, s = check_silu(gu, rs)
+        assert_close_int8(q, s, *ref_silu(gu, rs))
+    gh = gu.to(torch.float16)                              # fp16 saturates the huge ones to -inf
+    check_silu(torch.nan_to_num(gh, neginf=-65504.0), True)
 
 
 @pytest.mark.parametrize("m", [1, 16, 128, 1024, 4096])
@@ -135,7 +160,8 @@ def test_silu_mul_quant_config2(m):
     check_silu(gu, False, precise=False)
 
 
-@pytest.mark.parametrize("m,k", [(1, 2048), (16, 2048), (4096, 2048), (3, 13)])
+@pytest.mark.parametrize("m,k", [(1, 2048), (16, 2048), (4096, 2048), (3, 13), (5, 6144),
+                                 (2, 32768), (7, 1000)])
 def test_quant_per_token(m, k):
     say(f"quant_per_token m={m} k={k}")
     x = randn((m, k), 40 + m, 3.0)
@@ -144,6 +170,21 @@ def test_quant_per_token(m, k):
     assert np.array_equal(np_(q), q0) and np.array_equal(np_(s), s0)
     # torch's CPU division may differ by an ulp between CPU builds: the reference's tolerance
     assert_close_int8(q, s, *ref_quant(x.cpu().float()))
+
+
+def test_unaligned_rows_take_the_element_path():
+    """Rows that start off a 16-byte boundary are read and written element by element."""
+    say("quantizers unaligned pointers")
+    m, k = 5, 2048
+    xb, rb = randn((m * k + 1,), 70), randn((m * k + 1,), 71)
+    x, r = xb[1:].view(m, k), rb[1:].view(m, k)
+    w = randn((k,), 72, 0.1) + 1.0
+    check_norm(x, r, w)
+    gub = randn((m * 2 * k + 1,), 73)
+    check_silu(gub[1:].view(m, 2 * k), True)
+    q, s = fq.quant_per_token(x)
+    q0, s0 = o.quant_per_token(bits(x))
+    assert np.array_equal(np_(q), q0) and np.array_equal(np_(s), s0)
 
 
 def test_zero_row_gives_zero_scale_and_values():
