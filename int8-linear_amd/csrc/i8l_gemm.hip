@@ -49,46 +49,72 @@ struct Cols4 {
   float sb[4], bias[4];
 };
 
-// Branch-free loads of the epilogue operands of columns n..n+3: every address is chosen
-// with a select from pointers that are always valid (a scalar scale is re-read with stride
-// 0; an absent bias re-reads scale_b), and every bias dtype is read as 16-bit halves, so
-// all loads issue in one basic block and their latency is paid once.
+// Epilogue kinds.  EK_ANY reads the output dtype, the bias dtype and the scale layout from
+// the Epi at run time; the other kinds fix them at compile time (bf16 out, per-column
+// scale_b, no bias or a bf16 bias), which leaves the decode kernels' critical path free of
+// the dtype branches: every CU starts a short kernel with a cold instruction cache, so each
+// taken branch into code not yet fetched waits for a fetch from L2.
+enum { EK_ANY = 0, EK_BF16 = 1, EK_BF16_BBF16 = 2 };
+template <int EK>
+__device__ __forceinline__ int epi_out(const Epi& e) { return EK == EK_ANY ? e.out_dtype : I8L_BF16; }
+template <int EK>
+__device__ __forceinline__ int epi_bias(const Epi& e) {
+  return EK == EK_ANY ? e.bias_dtype : EK == EK_BF16 ? I8L_DTYPE_NONE : I8L_BF16;
+}
+template <int EK>
+__device__ __forceinline__ bool epi_sb_per_col(const Epi& e) { return EK == EK_ANY ? e.sb_per_col != 0 : true; }
+
+// The kind a call can use (host side).
+inline int epi_kind(const Epi& e) {
+  if (e.out_dtype != I8L_BF16 || !e.sb_per_col) return EK_ANY;
+  if (e.bias_dtype == I8L_DTYPE_NONE) return EK_BF16;
+  if (e.bias_dtype == I8L_BF16) return EK_BF16_BBF16;
+  return EK_ANY;
+}
+
+// The epilogue operands of columns n..n+3 (n a multiple of 4): one vector load for the four
+// scales and one for the four bias values.  The fast schedules require 16-byte aligned
+// per-column scales and bias, so these loads are aligned; the dtype tests are uniform.
+template <int EK = EK_ANY>
 __device__ __forceinline__ Cols4 load_cols4(const Epi& e, int64_t n) {
   Cols4 c;
-  if (e.out_dtype == I8L_I32) return c;
-  const int64_t sbs = e.sb_per_col ? 1 : 0;
-  const bool f32b = e.bias_dtype == I8L_F32;
-  const bool hasb = e.bias_dtype != I8L_DTYPE_NONE;
-  const uint16_t* bb = hasb ? (const uint16_t*)e.bias : (const uint16_t*)e.sb;
-  const int64_t bstep = hasb ? (f32b ? 2 : 1) : 0;
-  uint32_t lo[4], hi[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    c.sb[r] = e.sb[(n + r) * sbs];
-    const uint16_t* p = bb + (n + r) * bstep;
-    lo[r] = p[0];
-    hi[r] = p[f32b ? 1 : 0];
+  const int od = epi_out<EK>(e), bd = epi_bias<EK>(e);
+  if (od == I8L_I32) return c;
+  if (epi_sb_per_col<EK>(e)) {
+    const float4 v = *(const float4*)(e.sb + n);
+    c.sb[0] = v.x, c.sb[1] = v.y, c.sb[2] = v.z, c.sb[3] = v.w;
+  } else {
+    const float v = e.sb[0];
+    c.sb[0] = c.sb[1] = c.sb[2] = c.sb[3] = v;
   }
+  if (bd == I8L_F32) {
+    const float4 v = *(const float4*)((const float*)e.bias + n);
+    c.bias[0] = v.x, c.bias[1] = v.y, c.bias[2] = v.z, c.bias[3] = v.w;
+  } else if (bd == I8L_BF16 || bd == I8L_F16) {
+    const uint2 h = *(const uint2*)((const uint16_t*)e.bias + n);
+    const uint32_t w[4] = {h.x & 0xffffu, h.x >> 16, h.y & 0xffffu, h.y >> 16};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float fb = __uint_as_float(lo[r] | (hi[r] << 16));
-    const float bf = bf16_bits_to_f32(lo[r]);
-    const float hf = f16_bits_to_f32(lo[r]);
-    c.bias[r] = !hasb ? 0.0f : f32b ? fb : e.bias_dtype == I8L_BF16 ? bf : hf;
+    for (int r = 0; r < 4; ++r)
+      c.bias[r] = bd == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
+  } else {
+    c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = 0.0f;
   }
   return c;
 }
 
 // Four consecutive output columns n..n+3 of row m (n a multiple of 4; the fast schedules
 // require a 16-byte aligned output with 16-byte aligned rows).
+template <int EK = EK_ANY>
 __device__ __forceinline__ float load_sa(const Epi& e, int64_t m) {
-  if (e.out_dtype == I8L_I32) return 0.0f;
+  if (epi_out<EK>(e) == I8L_I32) return 0.0f;
   return e.sa[m * (e.sa_per_row ? 1 : 0)];
 }
 
+template <int EK = EK_ANY>
 __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i acc,
                                         const Cols4& c, float sam) {
-  if (e.out_dtype == I8L_I32) {
+  const int od = epi_out<EK>(e), bd = epi_bias<EK>(e);
+  if (od == I8L_I32) {
     *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
     return;
   }
@@ -98,16 +124,16 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
     float v = (float)acc[r];
     v = v * sam;
     v = v * c.sb[r];
-    if (e.bias_dtype != I8L_DTYPE_NONE) v = v + c.bias[r];
+    if (bd != I8L_DTYPE_NONE) v = v + c.bias[r];
     o[r] = v;
   }
-  if (e.out_dtype == I8L_F32) {
+  if (od == I8L_F32) {
     *(float4*)((float*)e.out + m * e.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
   } else {
     uint32_t lo, hi;
-    if (e.out_dtype == I8L_BF16) {
-      lo = f32_to_bf16_bits(o[0]) | ((uint32_t)f32_to_bf16_bits(o[1]) << 16);
-      hi = f32_to_bf16_bits(o[2]) | ((uint32_t)f32_to_bf16_bits(o[3]) << 16);
+    if (od == I8L_BF16) {
+      lo = f32x2_to_bf16x2_bits(o[0], o[1]);
+      hi = f32x2_to_bf16x2_bits(o[2], o[3]);
     } else {
       lo = f32_to_f16_bits(o[0]) | ((uint32_t)f32_to_f16_bits(o[1]) << 16);
       hi = f32_to_f16_bits(o[2]) | ((uint32_t)f32_to_f16_bits(o[3]) << 16);
@@ -116,13 +142,15 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
   }
 }
 
+template <int EK = EK_ANY>
 __device__ __forceinline__ void store4c(const Epi& e, int64_t m, int64_t n, v4i acc,
                                         const Cols4& c) {
-  store4s(e, m, n, acc, c, load_sa(e, m));
+  store4s<EK>(e, m, n, acc, c, load_sa<EK>(e, m));
 }
 
+template <int EK = EK_ANY>
 __device__ __forceinline__ void store4(const Epi& e, int64_t m, int64_t n, v4i acc) {
-  store4c(e, m, n, acc, load_cols4(e, n));
+  store4c<EK>(e, m, n, acc, load_cols4<EK>(e, n));
 }
 
 __device__ __forceinline__ void store1(const Epi& e, int64_t m, int64_t n, int32_t acc) {
@@ -277,6 +305,265 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
       else
         store4(e, m, n0 + NC * t + 4 * grp, s);
     }
+  }
+}
+
+// ------------------------------------------------------------------ weights-through-LDS schedule
+// Decode tile of 16*MT tokens x NC columns (NC = 16, 8 or 4).  Each wave owns one contiguous
+// K slice of `steps` steps of S = 64*KS bytes.  Per step it copies its NC x S weight bytes
+// into its own LDS buffer with global_load_lds_dwordx4: one instruction moves 1 KiB, whole
+// row segments of S bytes, so HBM sees full cache lines (the MFMA operand layout would read
+// 16 rows x 64 bytes per instruction instead).  LDS row r holds 16-byte chunk c at slot
+// c ^ (r & SWM), so the MFMA-layout reads (16 rows, one chunk each) spread over the banks.
+// The activations of the next step are loaded into registers while the current step
+// multiplies.  A wave only reads its own buffers, so its own vmcnt wait is the only
+// synchronisation until the cross-wave sum of the int32 partials.
+// With NC < 16, MFMA rows i and i+NC read the same weight row and only rows below NC are
+// stored.  Token rows past M read row 0 and are never stored.
+__host__ __device__ constexpr int wlds_bound(int mt, int ks) { return mt * ks <= 6 ? 1024 : 512; }
+
+// s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
+// no LDS read of the DMA'd data is scheduled above the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_wlds() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) int8_t lds_i8_t;
+
+template <int MT, int NC, int KS, int EK>
+__global__ void __launch_bounds__(wlds_bound(MT, KS))
+gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
+          Epi e, int steps, int nbuf) {
+  constexpr int S = 64 * KS;                 // K bytes per row per step
+  constexpr int CPR = S / 16;                // 16-byte chunks per row per step
+  // The swizzle XORs a slot with (row & SWM); SWM + 1 is a power of two dividing CPR, so
+  // every slot maps into the same row's [0, CPR) and no address leaves the row's slice.
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;                 // weight bytes per wave per step
+  constexpr int NI = SB / 1024;              // DMA instructions per wave per step
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int AL = MT * KS;                // activation loads per lane per step
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  // wave-uniform values live in scalar registers: the per-lane address work before the first
+  // load is then a few 32-bit operations
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)wave * steps * S;
+  int8_t* wbuf = lds + (size_t)wave * nbuf * SB;
+
+  // DMA sources of this lane: instruction t writes LDS bytes [t*1024, t*1024+1024) of the
+  // step buffer, lane l the 16 bytes at +16*l, which is row o / S, slot (o % S) / 16.
+  // Rows of a tile are < 16 apart, so their offsets fit 32 bits.
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  const int8_t* gsrc[NI];
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    gsrc[t] = Bw + (r * ldb32 + 16 * c);
+  }
+  // Token rows past M read the tile's first row (always valid); they are never stored.
+  const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
+  const int lda32 = (int)lda;
+  const int8_t* ap[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = 16 * i + r16;
+    ap[i] = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
+  }
+  // MFMA-layout read offsets of one step: row br, chunk 4s + grp
+  const int br = r16 % NC;
+  int rofs[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) rofs[s] = br * S + 16 * ((4 * s + grp) ^ (br & SWM));
+
+  v4i acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = v4i{0, 0, 0, 0};
+
+  v4i a0[KS][MT], a1[KS][MT];
+  // `fenced`: nothing of the previous step's MFMA work moves below the start of the issue,
+  // so the LDS reads of the buffer the step may overwrite have completed, and the loads go
+  // out before anything after them.  A single-step wave needs neither, and leaving the
+  // compiler free to interleave the address arithmetic with the loads issues them sooner.
+  auto issue = [&](v4i (&aa)[KS][MT], int step, bool fenced) {
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+    lds_i8_t* dst = (lds_i8_t*)(wbuf + (step % nbuf) * SB);
+    const int64_t ko = (int64_t)step * S;
+#pragma unroll
+    for (int t = 0; t < NI; ++t)
+      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) aa[s][i] = ld16(ap[i] + ko + 64 * s);
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](const v4i (&aa)[KS][MT], int step) {
+    const int8_t* base = wbuf + (step % nbuf) * SB;
+    v4i b[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[s] = *(const v4i*)(base + rofs[s]);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s], aa[s][i], acc[i], 0, 0, 0);
+  };
+
+  issue(a0, 0, steps > 1);
+  // The wave that stores fragment f (f % W == wave) loads its epilogue operands now, behind
+  // the first step, so their latency hides under the main loop.
+  Cols4 cl0;
+  float sa0 = 0.0f;
+  if (wave < MT && 4 * grp < NC) {
+    const int64_t m = m0 + 16 * wave + r16;
+    cl0 = load_cols4<EK>(e, n0 + 4 * grp);
+    sa0 = load_sa<EK>(e, m < e.M ? m : 0);
+  }
+  // Steady state: every step's loads are issued before the wait for the previous step, and
+  // the wait leaves exactly one step's loads outstanding.  The LDS reads of a step complete
+  // before its MFMAs, so its buffer is free when the step two later overwrites it.
+  int i = 0;
+  for (; i + 2 < steps; i += 2) {
+    issue(a1, i + 1, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a0, i);
+    issue(a0, i + 2, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a1, i + 1);
+  }
+  if (steps - i == 2) {
+    issue(a1, i + 1, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a0, i);
+    wait_vmcnt_wlds<0>();
+    compute(a1, i + 1);
+  } else {
+    wait_vmcnt_wlds<0>();
+    compute(a0, i);
+  }
+
+  // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
+  v4i* red = (v4i*)(lds + (size_t)W * nbuf * SB);  // [W][MT][64]
+  if (W > 1) {
+#pragma unroll
+    for (int f = 0; f < MT; ++f) red[(wave * MT + f) * 64 + lane] = acc[f];
+    __syncthreads();
+  }
+  for (int f = wave; f < MT; f += W) {
+    v4i sum;
+    if (W > 1) {
+      sum = red[f * 64 + lane];
+      for (int w = 1; w < W; ++w) sum += red[(w * MT + f) * 64 + lane];
+    } else {
+      sum = acc[0];
+#pragma unroll
+      for (int q = 1; q < MT; ++q)
+        if (q == f) sum = acc[q];
+    }
+    const int64_t m = m0 + 16 * f + r16;
+    if (m < e.M && 4 * grp < NC) {
+      if (f == wave)
+        store4s<EK>(e, m, n0 + 4 * grp, sum, cl0, sa0);
+      else
+        store4<EK>(e, m, n0 + 4 * grp, sum);
+    }
+  }
+}
+
+// The same tile when every wave's K slice is a single step (K == W * 64 * KS), with the
+// wave count and the epilogue kind fixed at compile time: the path from the first load to
+// the last store is straight-line code apart from the wave-uniform test of which waves
+// store, which matters in a kernel this short (see EK_ANY).
+template <int MT, int NC, int KS, int W, int EK>
+__global__ void __launch_bounds__(64 * W)
+gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
+           Epi e) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;
+  constexpr int NI = SB / 1024;
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  static_assert(MT <= W, "every fragment needs a storing wave");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)wave * S;
+  int8_t* wbuf = lds + (size_t)wave * SB;
+
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  lds_i8_t* dst = (lds_i8_t*)wbuf;
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                     16, 0, 0);
+  }
+  const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
+  const int lda32 = (int)lda;
+  v4i a[KS][MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = 16 * i + r16;
+    const int8_t* ap = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s][i] = ld16(ap + 64 * s);
+  }
+  // Epilogue operands of the fragment this wave stores (waves below MT), loaded behind the
+  // tile; lanes past NC columns load a valid neighbour and never store.
+  Cols4 cl;
+  float sam = 0.0f;
+  const int64_t mrow = m0 + 16 * wave + r16;
+  const int64_t ncol = n0 + 4 * (grp & (NC / 4 - 1));
+  if (wave < MT) {
+    cl = load_cols4<EK>(e, ncol);
+    sam = load_sa<EK>(e, mrow < e.M ? mrow : m0);
+  }
+  wait_vmcnt_wlds<0>();
+  const int br = r16 % NC;
+  v4i b[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) b[s] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+  v4i acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s], a[s][i], acc[i], 0, 0, 0);
+
+  // cross-wave sum (exact int32), then the storing waves apply the epilogue
+  v4i* red = (v4i*)(lds + (size_t)W * SB);  // [W][MT][64]
+#pragma unroll
+  for (int f = 0; f < MT; ++f) red[(wave * MT + f) * 64 + lane] = acc[f];
+  __syncthreads();
+  if (wave < MT) {
+    v4i sum = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[(w * MT + wave) * 64 + lane];
+    if (mrow < e.M && 4 * grp < NC) store4s<EK>(e, mrow, ncol, sum, cl, sam);
   }
 }
 
@@ -693,6 +980,33 @@ constexpr DmaTile kDma[] = {{256, 256, 64, 2, 2, 3}, {256, 256, 64, 2, 2, 4},
                             {256, 128, 128, 2, 4, 3}, {128, 256, 128, 2, 4, 3},
                             {128, 128, 128, 2, 2, 4}, {128, 128, 64, 2, 2, 4}};
 
+// Weights-through-LDS decode tiles (MT, NC, KS): bm = 16*MT, bn = NC, bk = 64*KS bytes of K
+// per wave step; the config's `stages` is 3 and K must split into warps x steps x bk.
+struct WldsTile {
+  int mt, nc, ks;
+};
+constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1, 8, 2},
+                              {1, 8, 4},  {1, 8, 6},  {1, 8, 8},  {1, 4, 4},  {1, 4, 8},
+                              {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4}};
+constexpr size_t kMaxLds = 160 * 1024;
+
+size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
+  const int64_t steps = K / ((int64_t)c.bk * c.warps);
+  const int nbuf = steps > 1 ? 2 : 1;
+  return (size_t)c.warps * nbuf * c.bn * c.bk + (size_t)c.warps * (c.bm / 16) * 1024;
+}
+
+bool wlds_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 3 || c.split_k != 1 || c.bm > 32 || c.warps < 1 || c.warps > 16) return false;
+  bool built = false;
+  for (auto t : kWlds)
+    if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
+        c.warps * 64 <= wlds_bound(t.mt, t.ks))
+      built = true;
+  if (!built || K <= 0 || K % ((int64_t)c.bk * c.warps)) return false;
+  return wlds_lds_bytes(c, K) <= kMaxLds;
+}
+
 int dma_index(const i8l_config& c) {
   if (c.stages < 3 || c.split_k != 1 || c.group_m < 1) return -1;
   for (int i = 0; i < (int)(sizeof(kDma) / sizeof(kDma[0])); ++i) {
@@ -725,6 +1039,89 @@ hipError_t launch_stream_u(const int8_t* a, int64_t lda, const int8_t* b, int64_
   else
     hipLaunchKernelGGL((gemm_stream<MT, NT, 1, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
   return hipGetLastError();
+}
+
+template <int MT, int NC, int KS, int EK>
+hipError_t launch_wlds_k(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  auto kern = gemm_wlds<MT, NC, KS, EK>;
+  const size_t shm = wlds_lds_bytes(c, K);
+  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kMaxLds);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  const int steps = (int)(K / ((int64_t)c.bk * c.warps));
+  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
+                     steps > 1 ? 2 : 1);
+  return hipGetLastError();
+}
+
+template <int MT, int NC, int KS, int W, int EK>
+hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  auto kern = gemm_wlds1<MT, NC, KS, W, EK>;
+  const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * 1024;
+  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
+  if (!attr_set && shm > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)shm);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
+  return hipGetLastError();
+}
+
+// Single-step launches for the (waves, step) pairs built: K = 64 * KS * W.
+template <int MT, int NC, int KS, int EK>
+hipError_t launch_wlds1_w(int W, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  if constexpr (KS <= 8) {
+    if (W == 4 && (KS == 4 || KS == 8)) return launch_wlds1_k<MT, NC, KS, 4, EK>(a, lda, b, ldb, e, st);
+    if (W == 8) return launch_wlds1_k<MT, NC, KS, 8, EK>(a, lda, b, ldb, e, st);
+    if (W == 16 && KS <= 6) return launch_wlds1_k<MT, NC, KS, 16, EK>(a, lda, b, ldb, e, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+bool wlds1_built(int W, int ks) {
+  return (W == 4 && (ks == 4 || ks == 8)) || W == 8 || (W == 16 && ks <= 6);
+}
+
+template <int MT, int NC, int KS>
+hipError_t launch_wlds_t(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  if (K == (int64_t)c.bk * c.warps && wlds1_built(c.warps, KS)) {
+    switch (epi_kind(e)) {
+      case EK_BF16: return launch_wlds1_w<MT, NC, KS, EK_BF16>(c.warps, a, lda, b, ldb, e, st);
+      case EK_BF16_BBF16:
+        return launch_wlds1_w<MT, NC, KS, EK_BF16_BBF16>(c.warps, a, lda, b, ldb, e, st);
+      default: return launch_wlds1_w<MT, NC, KS, EK_ANY>(c.warps, a, lda, b, ldb, e, st);
+    }
+  }
+  switch (epi_kind(e)) {
+    case EK_BF16: return launch_wlds_k<MT, NC, KS, EK_BF16>(c, a, lda, b, ldb, e, K, st);
+    case EK_BF16_BBF16: return launch_wlds_k<MT, NC, KS, EK_BF16_BBF16>(c, a, lda, b, ldb, e, K, st);
+    default: return launch_wlds_k<MT, NC, KS, EK_ANY>(c, a, lda, b, ldb, e, K, st);
+  }
+}
+
+hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                       int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  const int mt = c.bm / 16, nc = c.bn, ks = c.bk / 64;
+#define I8L_WLDS(MT_, NC_, KS_)                                                             \
+  if (mt == MT_ && nc == NC_ && ks == KS_) return launch_wlds_t<MT_, NC_, KS_>(c, a, lda, b, ldb, e, K, st);
+  I8L_WLDS(1, 16, 2) I8L_WLDS(1, 16, 4) I8L_WLDS(1, 16, 6) I8L_WLDS(1, 16, 8)
+  I8L_WLDS(1, 8, 2) I8L_WLDS(1, 8, 4) I8L_WLDS(1, 8, 6) I8L_WLDS(1, 8, 8)
+  I8L_WLDS(1, 4, 4) I8L_WLDS(1, 4, 8)
+  I8L_WLDS(2, 16, 2) I8L_WLDS(2, 16, 4) I8L_WLDS(2, 8, 2) I8L_WLDS(2, 8, 4)
+#undef I8L_WLDS
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
@@ -821,6 +1218,31 @@ int elt_size(int dt) { return dt == I8L_BF16 || dt == I8L_F16 ? 2 : 4; }
 
 void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   *c = i8l_config{0, 0, 0, 0, 0, 1, 1};
+  if (M <= 32 && K % 128 == 0) {
+    // weights through LDS: 16 (or, for narrow N, 8) columns a workgroup, the K split over
+    // up to 16 waves in one or more steps of up to 512 bytes
+    const int mt = M <= 16 ? 1 : 2;
+    const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : (N % 8 == 0 ? 8 : 4);
+    const int64_t k64 = K / 64;
+    const int kss[] = {8, 6, 4, 2};
+    // first choice: every wave's slice is one step (8, 16 or 4 waves); else 16 waves with
+    // the largest step that divides their slices
+    for (int W : {8, 16, 4})
+      for (int ks : kss) {
+        const i8l_config t{16 * mt, nc, 64 * ks, W, 3, 1, 1};
+        if (k64 == (int64_t)W * ks && wlds_ok(t, K)) {
+          *c = t;
+          return;
+        }
+      }
+    for (int ks : kss) {
+      const i8l_config t{16 * mt, nc, 64 * ks, 16, 3, 1, 1};
+      if (wlds_ok(t, K)) {
+        *c = t;
+        return;
+      }
+    }
+  }
   if (M <= 128) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
     // enough waves that each owns only a few 64-byte K steps, as many as fit a workgroup
@@ -875,7 +1297,7 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
               c.bm, c.bn, c.bk);
     return I8L_UNSUPPORTED;
   }
-  if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0) {
+  if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && !wlds_ok(c, K)) {
     set_error("config %dx%dx%d w%d s%d g%d k%d is not built into this library", c.bm, c.bn,
               c.bk, c.warps, c.stages, c.group_m, c.split_k);
     return I8L_UNSUPPORTED;
@@ -959,6 +1381,16 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     err = hipGetLastError();
   } else if (c.stages == 1) {
     err = launch_stream(c, a, stride_am, b, stride_bn, e, (int)K, hs);
+  } else if (c.stages == 3 && c.bm <= 32) {
+    // the schedule keeps in-tile row offsets in 32 bits
+    if (stride_am > INT32_MAX / 32 || stride_bn > INT32_MAX / 16) {
+      const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
+      hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
+                         stride_bk, stride_bn, e, K);
+      err = hipGetLastError();
+    } else {
+      err = launch_wlds(c, a, stride_am, b, stride_bn, e, K, hs);
+    }
   } else if (c.stages == 2) {
     err = launch_staged(staged_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   } else {

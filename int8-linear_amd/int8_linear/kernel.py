@@ -36,11 +36,16 @@ class NotSupported(Exception):
 class Config:
     """One GEMM launch configuration (reference kernel.py:49-60), in MI355X terms.
 
-    stages == 1 is the decode (weight-streaming) schedule: a workgroup of `warps` waves
-    covers bm tokens x bn columns and splits K across its waves, each taking 64-byte steps,
-    so bk == 64 * warps.  stages == 2 is the prefill schedule: a bm x bn macro tile staged
-    through double-buffered LDS, K in bk-byte steps, `warps` waves, `group_m` rows of tiles
-    walked together.  A configuration the library was not built with raises NotSupported.
+    Decode schedules (bm <= 128 tokens a workgroup, bn <= 32 columns):
+      stages == 1: weights streamed into MFMA registers; `warps` waves split K in 64-byte
+        steps, so bk == 64 * warps.
+      stages == 3, bm <= 32: weights copied through LDS with direct-to-LDS loads; each of the
+        `warps` waves owns one K slice taken bk bytes per step (K a multiple of bk * warps).
+    Prefill schedules (bm x bn macro tiles of 128 or 256, K in bk-byte steps, `group_m`
+    rows of tiles walked together):
+      stages == 2: double-buffered LDS staged through registers;
+      stages >= 3, bm >= 128: a ring of `stages` LDS buffers filled by direct-to-LDS loads.
+    A configuration the library was not built with raises NotSupported.
     """
 
     bm: int

@@ -40,9 +40,12 @@ def test_library_binary_is_built_for_gfx950_only():
 
 
 def test_default_config_regimes():
-    d = default_config(16, 4096, 2048)
-    assert d.stages == 1 and d.bm == 16 and d.bk == 64 * d.warps and 2048 % d.bk == 0
+    d = default_config(16, 4096, 2048)                      # weights through LDS
+    assert d.stages == 3 and d.bm == 16 and 2048 % (d.bk * d.warps) == 0
     assert default_config(17, 4096, 2048).bm == 32          # one tile covers M=17
+    assert default_config(1, 2048, 6144).bn == 8            # narrow N: 8 columns a workgroup
+    s = default_config(64, 4096, 2048)                      # register-streamed weights
+    assert s.stages == 1 and s.bm == 64 and s.bk == 64 * s.warps
     assert default_config(128, 2048, 6144).bm == 128
     p = default_config(4096, 28672, 4096)
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
@@ -55,7 +58,11 @@ def test_supported_decline_rule_matches_reference():
     # kernel.py:228-229 of the reference: N % bn or K % bk declines
     assert not kernel.supported(4, 64, 100)
     assert kernel.supported(16, 4096, 2048)
-    assert not kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 3, 1))  # 3 stages: not built
+    assert not kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 3, 1))  # 64-byte steps: not built
+    assert kernel.supported(16, 4096, 2048, Config(16, 16, 256, 8, 3, 1))     # through LDS, 1 step
+    assert kernel.supported(16, 4096, 2048, Config(16, 16, 128, 4, 3, 1))     # 4 steps a wave
+    assert not kernel.supported(16, 4096, 2048, Config(16, 16, 384, 4, 3, 1))  # K % (bk*warps)
+    assert not kernel.supported(16, 4096, 2048, Config(16, 16, 512, 16, 3, 1))  # LDS > 160 KiB
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 4, 2, 8))
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 4, 8))   # DMA ring of 4

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from helpers import bits, ints, np_, offset_ints, say
-from int8_linear import Config, NotSupported, w8a8_mm
+from int8_linear import Config, NotSupported, kernel, w8a8_mm
 from int8_linear.operands import operands, seed_of
 from int8_linear.shapes import SHAPES
 from oracle import oracle as o
@@ -85,12 +85,46 @@ def test_exact_under_other_tilings(config, m):
     assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
 
 
+# The weights-through-LDS decode schedule (stages 3, bm <= 32): every built tile, with one,
+# two, three and four K steps a wave (the ring's even and odd tails), 16/8/4 columns a
+# workgroup, ragged M.
+WLDS = [(mt, nc, ks) for mt, nc, ks in
+        [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
+         (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4)]]
+
+
+@pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
+@pytest.mark.parametrize("steps", [1, 2, 3, 4])
+@pytest.mark.parametrize("waves", [4, 8, 16])
+def test_weights_through_lds_schedule(tile, steps, waves):
+    mt, nc, ks = tile
+    k, n = 64 * ks * waves * steps, 512
+    cfg = Config(16 * mt, nc, 64 * ks, waves, 3, 1)
+    if not kernel.supported(16 * mt, n, k, cfg):
+        pytest.skip(f"{cfg.name} is not built for K={k}")
+    for m in ((1, 5, 16) if mt == 1 else (17, 32)):
+        say(f"w8a8_mm wlds m={m} k={k} n={n} config={cfg.name}")
+        a, w = ints((m, k), 11 + m), ints((n, k), 12)
+        one = torch.ones(1, device="cuda")
+        got = w8a8_mm(a, w.t(), one, one, raw=True, config=cfg)
+        assert np.array_equal(np_(got), o.gemm_i32(np_(a), np_(w)))
+        g = torch.Generator().manual_seed(m)
+        sa = (torch.rand((m, 1), generator=g) * 1e-2 + 1e-3).cuda()
+        sb = (torch.rand((n, 1), generator=g) * 1e-2 + 1e-3).cuda()
+        for bias in (None, torch.randn(n, generator=g).to(torch.bfloat16).cuda()):
+            out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, bias, config=cfg)
+            assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, bias, torch.bfloat16))
+        out = w8a8_mm(a, w.t(), sa, sb, torch.float16, config=cfg)     # the generic epilogue
+        assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.float16))
+
+
+@pytest.mark.parametrize("m", [37, 13])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("per_row", [True, False])
 @pytest.mark.parametrize("per_col", [True, False])
 @pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float16, torch.float32])
-def test_scaled_output_matches_oracle_and_float64(dtype, per_row, per_col, bias_dtype):
-    m, k, n = 37, 2048, 1024
+def test_scaled_output_matches_oracle_and_float64(m, dtype, per_row, per_col, bias_dtype):
+    k, n = 2048, 1024
     say(f"w8a8_mm scaled m={m} {dtype} row={per_row} col={per_col} bias={bias_dtype}")
     a, w = ints((m, k), 5), ints((n, k), 6)
     g = torch.Generator().manual_seed(7)
