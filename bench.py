@@ -39,6 +39,8 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
 DECODE_M = [1, 2, 4, 8, 16, 17, 32, 64, 128]
 PREFILL_M = [512, 1024, 2048, 4096]
 QUANT_M = [1, 16, 128, 1024, 4096]
+STANDIN_M = [1, 8, 32, 128]
+STANDIN_PREFILL_M = 4096
 ROTATE_BYTES = 768 << 20
 METRIC = "W8A8 linear µs & % of HBM/int8 roofline, M=1-4096; µs per decoder-layer stand-in"
 
@@ -210,6 +212,8 @@ def main() -> int:
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
+    ap.add_argument("--only", choices=["quant", "prefill", "standin"], default=None,
+                    help="run one extra section alone (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
@@ -227,6 +231,10 @@ def main() -> int:
         rf = roofline_config0(dev)
         cal = copy_calibration(dev)
         print(json.dumps({"roofline": rf, "calibration": cal}), flush=True)
+        return 0
+    if args.only:
+        fn = {"quant": bench_quant, "prefill": bench_prefill, "standin": bench_standin}[args.only]
+        print(json.dumps({args.only: fn(dev)}), flush=True)
         return 0
     shapes = SHAPES["qwen3-1.7b-vllm"]
     sw = Sweep(shapes, DECODE_M, dev)
@@ -301,6 +309,7 @@ def main() -> int:
         result["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
         result["quant"] = bench_quant(dev)
         result["prefill"] = bench_prefill(dev)
+        result["standin"] = bench_standin(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -329,6 +338,29 @@ def bench_quant(dev) -> dict:
         del xs, rs, gus
     return {"cols": ["M", "add_rmsnorm_quant_us", "hbm_frac", "silu_mul_quant_us", "hbm_frac"],
             "rows": rows}
+
+
+def bench_standin(dev) -> dict:
+    """the 28-layer Qwen3-1.7B decoder stand-in, one step per graph
+    replay, microseconds per decoder layer, at decode M and one 4096-token prefill."""
+    import torch
+
+    from int8_linear import standin
+    base = standin.DecoderStandIn(1, generator_device="cuda")   # 1.41 GB of layer weights
+    wbytes = base.weight_bytes() / len(base.layers)
+    rows = []
+    for m in STANDIN_M + [STANDIN_PREFILL_M]:
+        st = base.with_batch(m, seed=m)
+        us = standin.per_layer_us(st, windows=5)
+        rows.append([m, round(us, 2), round(wbytes / (us * 1e-6) / 1e9, 1)])
+        log(f"standin M={m}: {us:.2f} us per layer")
+        del st
+    del base
+    torch.cuda.empty_cache()
+    return {"cols": ["M", "us_per_layer", "weight_GBps"], "rows": rows,
+            "layers": standin.LAYERS, "weight_bytes_per_layer": int(wbytes),
+            "step": "add_rmsnorm_quant > qkv > quant(q cols) > o > add_rmsnorm_quant > gate_up "
+                    "> silu_mul_quant > down, one HIP graph per 28-layer step"}
 
 
 def bench_prefill(dev) -> dict:

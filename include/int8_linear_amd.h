@@ -123,12 +123,15 @@ int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale,
                        int32_t round_silu, int32_t precise_div, void* stream);
 
 /*
- * Plain per-token int8 quantize of a bf16/f16 [M,H] contiguous tensor (the quantizer of
- * int8_linear/fused_quant.py:41-53 on its own).  Stands in for vLLM's scaled_int8_quant,
- * which the reference's decoder stand-in calls on the o_proj input
- * (bench/fuse_quant.py:234, bench/situ_tune.py:110).
+ * Plain per-token int8 quantize of a bf16/f16 [M,H] tensor whose rows lie ldx elements apart
+ * (ldx >= H; ldx == H is a contiguous tensor): the quantizer of
+ * int8_linear/fused_quant.py:41-53 on its own.  Stands in for vLLM's scaled_int8_quant, which
+ * the reference's decoder stand-in calls on the o_proj input (bench/fuse_quant.py:234,
+ * bench/situ_tune.py:110).  With ldx > H it quantizes a column slice in place, e.g. the
+ * q columns of a qkv output, which the reference first copies with .contiguous()
+ * (bench/fuse_quant.py:233).
  */
-int i8l_quant_per_token(const void* x, int8_t* q, float* scale,
+int i8l_quant_per_token(const void* x, int64_t ldx, int8_t* q, float* scale,
                         int64_t M, int64_t H, int32_t act_dtype,
                         int32_t precise_div, void* stream);
 

@@ -388,14 +388,14 @@ silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
 // ------------------------------------------------------------------ plain per-token quant
 template <int J, int DT, bool VEC>
 __global__ void __launch_bounds__(1024)
-quant_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scale,
-             int64_t M, int H, int nw, int rpb, int precise) {
+quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
+             float* __restrict__ scale, int64_t M, int H, int nw, int rpb, int precise) {
   __shared__ float fsh[kMaxWaves];
   const RowPos p = row_pos(nw, rpb);
   if (p.row >= M) return;
   float y[J][8];
 #pragma unroll
-  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + p.row * H, chunk_base<J>(p, j), H, y[j]);
+  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + p.row * ldx, chunk_base<J>(p, j), H, y[j]);
   quantize_store<J, VEC>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
 }
 
@@ -489,10 +489,10 @@ void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint1
 
 template <int DT>
 void launch_quant(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
-                  int8_t* q, float* scale, int64_t M, int H, int precise) {
+                  int64_t ldx, int8_t* q, float* scale, int64_t M, int H, int precise) {
 #define I8L_QUANT(J_, V_)                                                                   \
-  hipLaunchKernelGGL((quant_kernel<J_, DT, V_>), grid, block_of(g), 0, st, x, q, scale, M, H, \
-                     g.nw, g.rpb, precise)
+  hipLaunchKernelGGL((quant_kernel<J_, DT, V_>), grid, block_of(g), 0, st, x, ldx, q, scale, \
+                     M, H, g.nw, g.rpb, precise)
   if (!vec) I8L_QUANT(4, false);
   else if (g.j == 1) I8L_QUANT(1, true);
   else if (g.j == 2) I8L_QUANT(2, true);
@@ -573,10 +573,12 @@ extern "C" int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale, 
   return hip_status(hipGetLastError(), "silu_mul_quant launch");
 }
 
-extern "C" int i8l_quant_per_token(const void* x, int8_t* q, float* scale, int64_t M, int64_t H,
-                                   int32_t act_dtype, int32_t precise_div, void* stream) {
-  if (M < 0 || H <= 0) {
-    set_error("quant_per_token: bad sizes M=%lld H=%lld", (long long)M, (long long)H);
+extern "C" int i8l_quant_per_token(const void* x, int64_t ldx, int8_t* q, float* scale,
+                                   int64_t M, int64_t H, int32_t act_dtype, int32_t precise_div,
+                                   void* stream) {
+  if (M < 0 || H <= 0 || ldx < H) {
+    set_error("quant_per_token: bad sizes M=%lld H=%lld ldx=%lld", (long long)M, (long long)H,
+              (long long)ldx);
     return I8L_INVALID_ARG;
   }
   if (!act_ok(act_dtype)) {
@@ -589,12 +591,14 @@ extern "C" int i8l_quant_per_token(const void* x, int8_t* q, float* scale, int64
   }
   if (M == 0) return I8L_OK;
   const int h = (int)H;
-  const bool vec = h % 8 == 0 && a16(x) && a16(q);
+  const bool vec = h % 8 == 0 && ldx % 8 == 0 && a16(x) && a16(q);
   const Geom g = flat_geom(M, h, vec);
   const hipStream_t st = (hipStream_t)stream;
   if (act_dtype == I8L_BF16)
-    launch_quant<I8L_BF16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, q, scale, M, h, precise_div);
+    launch_quant<I8L_BF16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, ldx, q, scale, M, h,
+                           precise_div);
   else
-    launch_quant<I8L_F16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, q, scale, M, h, precise_div);
+    launch_quant<I8L_F16>(g, vec, grid_of(M, g), st, (const uint16_t*)x, ldx, q, scale, M, h,
+                          precise_div);
   return hip_status(hipGetLastError(), "quant_per_token launch");
 }

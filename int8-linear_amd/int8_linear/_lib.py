@@ -54,7 +54,7 @@ def lib() -> ctypes.CDLL:
     L.i8l_add_rmsnorm_quant.argtypes = [_P, _P, _P, ctypes.c_float, _P, _P, _P, _I64, _I64, _I32,
                                         _I32, _I32, _P]
     L.i8l_silu_mul_quant.argtypes = [_P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P]
-    L.i8l_quant_per_token.argtypes = [_P, _P, _P, _I64, _I64, _I32, _I32, _P]
+    L.i8l_quant_per_token.argtypes = [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P]
     for name in EXPORTS[:-2]:
         getattr(L, name).restype = ctypes.c_int
     L.i8l_last_error.restype = ctypes.c_char_p

@@ -90,15 +90,18 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
 
     The quantizer of the two fused kernels on its own, with vLLM scaled_int8_quant's
     convention; it quantizes the o_proj input, which has no kernel before it to fuse into.
+    x may be a column slice of a wider tensor (unit column stride, any row stride), such
+    as the q columns of a qkv output: it is read in place, with no copy.
     """
-    assert x.is_contiguous() and x.dim() == 2
+    assert x.dim() == 2 and (x.stride(1) == 1 or x.shape[1] <= 1)
     M, K = x.shape
     act = _act_code(x, "x")
     q = torch.empty((M, K), dtype=torch.int8, device=x.device)
     s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
     if M and K:
-        status = _lib.lib().i8l_quant_per_token(x.data_ptr(), q.data_ptr(), s.data_ptr(), M, K,
-                                                act, int(bool(precise_div)), _lib.stream_of(x))
+        ldx = x.stride(0) if M > 1 else K
+        status = _lib.lib().i8l_quant_per_token(x.data_ptr(), ldx, q.data_ptr(), s.data_ptr(), M,
+                                                K, act, int(bool(precise_div)), _lib.stream_of(x))
         _lib.check(status, NotSupported)
     return q, s
 

@@ -1,0 +1,131 @@
+"""The 28-layer Qwen3-1.7B decoder stand-in, built from this package's kernels.
+
+The reference measures its kernels in a stand-in for the served model's decode step
+(AshrithaG/int8-linear, bench/fuse_quant.py:184-240, Stack.fused; also
+bench/situ_tune.py:77-104).  The stand-in has 28 decoder layers of the model's four int8
+linears, each layer with its own weights, with the fused quantizers and residual adds
+between them. Attention is left out: the q columns of the qkv projection go straight to
+o_proj. Per layer:
+
+    add_rmsnorm_quant -> qkv_proj -> quant_per_token(q columns) -> o_proj
+    -> add_rmsnorm_quant -> gate_up_proj -> silu_mul_quant -> down_proj
+
+The first layer normalizes without a residual, as `rmsnorm_quant` does.
+
+The reference slices the q columns with .contiguous() and then quantizes them
+(bench/fuse_quant.py:233-234). Here the per-token quantizer reads the slice in place, so
+each layer issues 8 kernels instead of 9, and the values are the same.
+
+Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
+  * x ~ N(0, 1) bf16;
+  * norm weight all ones;
+  * per layer and linear, int8 weights uniform in [-127, 127] and per-channel scales
+    rand * 1e-3 + 1e-4, all from one seeded generator.
+A layer carries 50.3 MB of weights, so 28 layers (1.41 GB) cannot stay in the 256 MB
+Infinity Cache: every step streams them from HBM, as the served model does.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from int8_linear import fused_quant as fq
+from int8_linear.kernel import w8a8_mm
+
+HIDDEN = 2048
+INTER = 6144
+Q_COLS = 2048          # q heads x head dim: the slice of qkv that feeds o_proj
+LAYERS = 28
+EPS = 1e-6
+# (K, N) of each linear, as vLLM runs Qwen3-1.7B (merged qkv and gate/up)
+SHAPES = {"qkv_proj": (HIDDEN, 4096), "o_proj": (HIDDEN, HIDDEN),
+          "gate_up_proj": (HIDDEN, 2 * INTER), "down_proj": (INTER, HIDDEN)}
+
+
+class DecoderStandIn:
+    """`layers` decoder layers' linears and quantizers for a batch of m tokens."""
+
+    def __init__(self, m: int, layers: int = LAYERS, seed: int = 0,
+                 device: str | torch.device = "cuda", generator_device: str = "cpu"):
+        g = torch.Generator(device=generator_device).manual_seed(seed)
+        dev = torch.device(device)
+        self.m = m
+        self.x = torch.randn((m, HIDDEN), generator=g, device=generator_device).to(
+            torch.bfloat16).to(dev)
+        self.norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
+        self.layers: list[dict[str, tuple[torch.Tensor, torch.Tensor]]] = []
+        for _ in range(layers):
+            layer = {}
+            for name, (k, n) in SHAPES.items():
+                w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8,
+                                  device=generator_device).to(dev)
+                s = (torch.rand((n, 1), generator=g, device=generator_device) * 1e-3
+                     + 1e-4).to(dev)
+                layer[name] = (w, s)
+            self.layers.append(layer)
+
+    def with_batch(self, m: int, seed: int = 0) -> "DecoderStandIn":
+        """The same layers (weights shared, not copied) with a new batch of m tokens."""
+        other = object.__new__(DecoderStandIn)
+        other.__dict__.update(self.__dict__)
+        g = torch.Generator().manual_seed(seed)
+        other.m = m
+        other.x = torch.randn((m, HIDDEN), generator=g).to(torch.bfloat16).to(self.x.device)
+        return other
+
+    def weight_bytes(self) -> int:
+        return sum(w.numel() + 4 * s.numel() for layer in self.layers for w, s in layer.values())
+
+    def mm(self, layer, name: str, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+        w, ws = layer[name]
+        return w8a8_mm(q, w.t(), s, ws, torch.bfloat16)
+
+    def forward(self) -> torch.Tensor:
+        """One step through every layer; returns the last down_proj output [m, HIDDEN]."""
+        res = self.x
+        q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
+        h = None
+        for i, layer in enumerate(self.layers):
+            if i:
+                q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
+            a = self.mm(layer, "qkv_proj", q, s)
+            q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
+            h = self.mm(layer, "o_proj", q, s)
+            q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
+            gu = self.mm(layer, "gate_up_proj", q, s)
+            q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)
+            h = self.mm(layer, "down_proj", q, s)
+        return h
+
+
+def per_layer_us(stack: DecoderStandIn, windows: int = 5, min_window_ms: float = 20.0) -> float:
+    """Median microseconds per decoder layer, with the whole step captured as one HIP graph
+    and replayed (the reference's discipline, bench/situ_tune.py:127-154)."""
+    import statistics
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack.forward()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack.forward()
+    graph.replay()
+    torch.cuda.synchronize()
+
+    def window(reps: int) -> float:
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        stop.record()
+        stop.synchronize()
+        return start.elapsed_time(stop) * 1e3 / reps / len(stack.layers)
+
+    one_ms = window(1) * len(stack.layers) / 1e3
+    reps = max(3, int(min_window_ms / max(one_ms, 1e-3)))
+    times = [window(reps) for _ in range(windows)]
+    del graph
+    return statistics.median(times)

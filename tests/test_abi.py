@@ -90,7 +90,9 @@ def test_invalid_sizes_are_rejected_before_any_launch():
     assert st == _lib.UNSUPPORTED
     # M == 0 launches nothing and succeeds without touching any pointer
     assert L.i8l_silu_mul_quant(None, None, None, 0, 64, _lib.BF16, 1, 1, None) == _lib.OK
-    assert L.i8l_quant_per_token(None, None, None, 0, 64, _lib.BF16, 1, None) == _lib.OK
+    assert L.i8l_quant_per_token(None, 64, None, None, 0, 64, _lib.BF16, 1, None) == _lib.OK
+    # a row stride below the row length is an error
+    assert L.i8l_quant_per_token(None, 32, None, None, 2, 64, _lib.BF16, 1, None) == _lib.INVALID_ARG
 
 
 def test_config_name_format():

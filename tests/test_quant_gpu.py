@@ -172,6 +172,18 @@ def test_quant_per_token(m, k):
     assert_close_int8(q, s, *ref_quant(x.cpu().float()))
 
 
+@pytest.mark.parametrize("m,k,ld", [(1, 2048, 4096), (16, 2048, 4096), (128, 2048, 4096),
+                                    (5, 1000, 1003), (3, 13, 40)])
+def test_quant_per_token_reads_a_column_slice_in_place(m, k, ld):
+    """The q columns of a qkv output, quantized without a copy, equal the copied slice's."""
+    say(f"quant_per_token slice m={m} k={k} ld={ld}")
+    wide = randn((m, ld), 90 + m, 3.0)
+    view = wide[:, :k]
+    q, s = fq.quant_per_token(view)
+    q0, s0 = o.quant_per_token(bits(view.contiguous()))
+    assert np.array_equal(np_(q), q0) and np.array_equal(np_(s), s0)
+
+
 def test_unaligned_rows_take_the_element_path():
     """Rows that start off a 16-byte boundary are read and written element by element."""
     say("quantizers unaligned pointers")
