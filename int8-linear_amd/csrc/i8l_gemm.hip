@@ -921,6 +921,144 @@ gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B
   tile_epilogue<BM, BN, WM, WN, FA, FB>(e, acc, lds, m0, n0, wm, wn, lane, tid);
 }
 
+// ------------------------------------------------------------------ pipelined dma schedule
+// The dma schedule with the LDS fragment reads overlapped with the MFMAs.  A K step of BK
+// bytes is KK = BK/32 MFMA substeps; substep kk's MFMAs are issued one after another with the
+// reads of the next substep's fragments between them (one read after each MFMA), from two
+// register sets of one substep each.  Before the last substep of step t, each wave waits for
+// its DMA of step t+1 (vmcnt), the workgroup barrier makes step t+1 visible and frees the
+// buffer of step t-1 (whose last reads fed MFMAs before the barrier), and step t+S-1 is
+// requested into it; the last substep's MFMAs then overlap the reads of step t+1's first
+// substep.  The LDS traffic of each substep hides under the matrix work of the one before.
+template <int BM, int BN, int BK, int WM, int WN, int S>
+__global__ void __launch_bounds__(64 * WM * WN)
+gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
+          int64_t ldb, Epi e, int K, int group_m) {
+  constexpr int W = WM * WN;
+  constexpr int T = 64 * W;
+  constexpr int NCH = BK / 16;
+  constexpr int UNITS = (BM + BN) * NCH;
+  constexpr int J = UNITS / T;
+  static_assert(J * T == UNITS, "stage does not split over the waves");
+  static_assert(BM % (64 / NCH) == 0, "one DMA instruction must stay within A or B rows");
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FB = TM / 32, FA = TN / 32;
+  constexpr int KK = BK / 32;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int NM = FA * FB;                // MFMAs per substep
+  constexpr int NR = FA + FB;                // fragment reads per substep
+  static_assert(S >= 3, "the ring needs at least three buffers");
+
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int num_pid_m = (e.M + BM - 1) / BM;
+  const int num_pid_n = e.N / BN;
+  int pid_m, pid_n;
+  staged_tile(blockIdx.x, gridDim.x, num_pid_m, num_pid_n, group_m, pid_m, pid_n);
+  const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int8_t* gp[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int u = (j * W + wave) * 64 + lane;
+    const int row = u / NCH, chunk = (u % NCH) ^ swz<BK>(row);
+    gp[j] = row < BM ? A + min(m0 + row, (int64_t)e.M - 1) * lda + chunk * 16
+                     : B + (n0 + row - BM) * ldb + chunk * 16;
+  }
+  const int KT = K / BK;
+  auto dma = [&](int t) {
+    const int64_t k0 = (int64_t)min(t, KT - 1) * BK;
+    lds_i8* dst = (lds_i8*)(lds + (t % S) * STAGE + wave * 1024);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0, 0);
+  };
+
+  v16i acc[FA][FB];
+#pragma unroll
+  for (int a = 0; a < FA; ++a)
+#pragma unroll
+    for (int b = 0; b < FB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
+
+  const int frow = lane & 31, fhalf = lane >> 5;
+  int fofs[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) fofs[kk] = frow * BK + (((2 * kk + fhalf) ^ swz<BK>(frow)) * 16);
+  const int a_row = BM * BK + wn * TN * BK;
+  const int b_row = wm * TM * BK;
+
+  v4i f0a[FA], f0b[FB], f1a[FA], f1b[FB];
+  auto rd = [&](v4i (&fa)[FA], v4i (&fb)[FB], int t, int kk) {
+    const int8_t* base = lds + (t % S) * STAGE;
+#pragma unroll
+    for (int a = 0; a < FA; ++a) fa[a] = *(const v4i*)(base + a_row + a * 32 * BK + fofs[kk]);
+#pragma unroll
+    for (int b = 0; b < FB; ++b) fb[b] = *(const v4i*)(base + b_row + b * 32 * BK + fofs[kk]);
+  };
+  auto mm = [&](const v4i (&fa)[FA], const v4i (&fb)[FB]) {
+#pragma unroll
+    for (int a = 0; a < FA; ++a)
+#pragma unroll
+      for (int b = 0; b < FB; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
+  };
+  // one substep: its MFMAs with the next substep's reads between them
+  auto overlap = [&](const v4i (&ca)[FA], const v4i (&cb)[FB], v4i (&na)[FA], v4i (&nb)[FB],
+                     int t, int kk) {
+    __builtin_amdgcn_sched_barrier(0);
+    rd(na, nb, t, kk);
+    mm(ca, cb);
+    constexpr int P = NR < NM ? NR : NM;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+    }
+    if (NM > P) __builtin_amdgcn_sched_group_barrier(0x008, NM - P, 0);
+    if (NR > P) __builtin_amdgcn_sched_group_barrier(0x100, NR - P, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Steps requested before the wait in step t: 0 .. t+S-2; step t+1 must be complete.
+  auto turn = [&](int t) {
+    wait_vmcnt<J * (S - 3)>();
+    lds_barrier();
+    dma(t + S - 1);
+  };
+  // One K step from fragment set 0 (holding substep 0); leaves step t+1's substep 0 in set 0
+  // when `more`.  KK is even, so the substeps alternate 0,1,0,1,... and end in set 1.
+  auto kstep = [&](int t, bool more) {
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk) {
+      if (kk % 2 == 0) overlap(f0a, f0b, f1a, f1b, t, kk + 1);
+      else overlap(f1a, f1b, f0a, f0b, t, kk + 1);
+    }
+    if (more) {
+      turn(t);
+      overlap(f1a, f1b, f0a, f0b, t + 1, 0);
+    } else {
+      mm(f1a, f1b);
+    }
+  };
+  static_assert(KK % 2 == 0, "substeps alternate between the two fragment sets");
+
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t) dma(t);
+  wait_vmcnt<J * (S - 2)>();
+  lds_barrier();
+  rd(f0a, f0b, 0, 0);
+  for (int t = 0; t + 1 < KT; ++t) kstep(t, true);
+  kstep(KT - 1, false);
+  wait_vmcnt<0>();
+  lds_barrier();
+  tile_epilogue<BM, BN, WM, WN, FA, FB>(e, acc, lds, m0, n0, wm, wn, lane, tid);
+}
+
 // ------------------------------------------------------------------ generic schedule
 __global__ void __launch_bounds__(256)
 gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_t* __restrict__ B,
@@ -951,12 +1089,13 @@ struct StagedTile {
 constexpr StreamTile kStream[] = {{1, 1, 16}, {2, 1, 16}, {4, 1, 16}, {8, 1, 16}, {1, 2, 16},
                                   {2, 2, 16}, {4, 2, 16}, {1, 1, 8},  {2, 1, 8},  {1, 1, 4}};
 // (BM, BN, BK, WM, WN); the waves of a workgroup are laid out WM (tokens) x WN (columns).
+// (256x256 tiles with 4 waves, or with 128-byte K steps, spill the register file and are
+// not built.)
 constexpr StagedTile kStaged[] = {{128, 128, 64, 2, 2},  {256, 128, 64, 2, 2},
-                                  {128, 256, 64, 2, 2},  {256, 256, 64, 2, 2},
-                                  {256, 256, 128, 2, 2}, {128, 128, 128, 2, 2},
-                                  {256, 256, 64, 2, 4},  {256, 256, 128, 2, 4},
-                                  {256, 128, 64, 2, 4},  {128, 256, 64, 2, 4},
-                                  {256, 128, 128, 2, 4}, {128, 256, 128, 2, 4}};
+                                  {128, 256, 64, 2, 2},  {128, 128, 128, 2, 2},
+                                  {256, 256, 64, 2, 4},  {256, 128, 64, 2, 4},
+                                  {128, 256, 64, 2, 4},  {256, 128, 128, 2, 4},
+                                  {128, 256, 128, 2, 4}};
 
 bool stream_ok(const i8l_config& c) {
   if (c.stages != 1 || c.split_k != 1 || c.bm % 16) return false;
@@ -974,11 +1113,12 @@ struct DmaTile {
   int bm, bn, bk, wm, wn, s;
 };
 // (BM, BN, BK, WM, WN, ring depth S); the config's `stages` field is S.
-constexpr DmaTile kDma[] = {{256, 256, 64, 2, 2, 3}, {256, 256, 64, 2, 2, 4},
-                            {256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
+constexpr DmaTile kDma[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                             {256, 128, 64, 2, 4, 4}, {128, 256, 64, 2, 4, 4},
                             {256, 128, 128, 2, 4, 3}, {128, 256, 128, 2, 4, 3},
-                            {128, 128, 128, 2, 2, 4}, {128, 128, 64, 2, 2, 4}};
+                            {128, 128, 128, 2, 2, 4}, {128, 128, 64, 2, 2, 4},
+                            {256, 256, 64, 2, 4, 5}, {256, 128, 64, 2, 4, 6},
+                            {128, 256, 64, 2, 4, 6}, {128, 128, 64, 2, 2, 8}};
 
 // Weights-through-LDS decode tiles (MT, NC, KS): bm = 16*MT, bn = NC, bk = 64*KS bytes of K
 // per wave step; the config's `stages` is 3 and K must split into warps x steps x bk.
@@ -1005,6 +1145,26 @@ bool wlds_ok(const i8l_config& c, int64_t K) {
       built = true;
   if (!built || K <= 0 || K % ((int64_t)c.bk * c.warps)) return false;
   return wlds_lds_bytes(c, K) <= kMaxLds;
+}
+
+// Direct-to-LDS tiles with the fragment reads overlapped with the MFMAs (gemm_dmap): the
+// config's `stages` is the ring depth S plus 8.
+constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
+                             {256, 256, 64, 2, 4, 5}, {256, 128, 64, 2, 4, 4},
+                             {128, 256, 64, 2, 4, 4}, {128, 256, 128, 2, 4, 3},
+                             {256, 128, 128, 2, 4, 3}, {128, 128, 64, 2, 2, 4},
+                             {128, 128, 128, 2, 2, 4}};
+constexpr int kPipelined = 8;
+
+int dmap_index(const i8l_config& c) {
+  if (c.stages < 3 + kPipelined || c.split_k != 1 || c.group_m < 1) return -1;
+  for (int i = 0; i < (int)(sizeof(kDmap) / sizeof(kDmap[0])); ++i) {
+    const auto& t = kDmap[i];
+    if (t.bm == c.bm && t.bn == c.bn && t.bk == c.bk && t.wm * t.wn == c.warps &&
+        t.s + kPipelined == c.stages)
+      return i;
+  }
+  return -1;
 }
 
 int dma_index(const i8l_config& c) {
@@ -1177,16 +1337,52 @@ hipError_t launch_dma_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
 hipError_t launch_dma(int idx, const i8l_config& c, const int8_t* a, int64_t lda,
                       const int8_t* b, int64_t ldb, const Epi& e, int K, hipStream_t st) {
   switch (idx) {
-    case 0: return launch_dma_t<256, 256, 64, 2, 2, 3>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 1: return launch_dma_t<256, 256, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 2: return launch_dma_t<256, 256, 64, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 3: return launch_dma_t<256, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 4: return launch_dma_t<256, 128, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 5: return launch_dma_t<128, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 6: return launch_dma_t<256, 128, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 7: return launch_dma_t<128, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 8: return launch_dma_t<128, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 9: return launch_dma_t<128, 128, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 0: return launch_dma_t<256, 256, 64, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 1: return launch_dma_t<256, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 2: return launch_dma_t<256, 128, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 3: return launch_dma_t<128, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 4: return launch_dma_t<256, 128, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 5: return launch_dma_t<128, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 6: return launch_dma_t<128, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 7: return launch_dma_t<128, 128, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 8: return launch_dma_t<256, 256, 64, 2, 4, 5>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 9: return launch_dma_t<256, 128, 64, 2, 4, 6>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 10: return launch_dma_t<128, 256, 64, 2, 4, 6>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 11: return launch_dma_t<128, 128, 64, 2, 2, 8>(a, lda, b, ldb, e, K, c.group_m, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int S>
+hipError_t launch_dmap_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                         const Epi& e, int K, int group_m, hipStream_t st) {
+  auto kern = gemm_dmap<BM, BN, BK, WM, WN, S>;
+  const size_t shm = std::max<size_t>((size_t)S * (BM + BN) * BK,
+                                      tile_epilogue_lds_bytes<BM, BN, WM, WN>());
+  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
+  if (!attr_set && shm > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)shm);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
+  return hipGetLastError();
+}
+
+hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t lda,
+                       const int8_t* b, int64_t ldb, const Epi& e, int K, hipStream_t st) {
+  switch (idx) {
+    case 0: return launch_dmap_t<256, 256, 64, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 1: return launch_dmap_t<256, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 2: return launch_dmap_t<256, 256, 64, 2, 4, 5>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 3: return launch_dmap_t<256, 128, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 4: return launch_dmap_t<128, 256, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 5: return launch_dmap_t<128, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 6: return launch_dmap_t<256, 128, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 7: return launch_dmap_t<128, 128, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 8: return launch_dmap_t<128, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1197,15 +1393,12 @@ hipError_t launch_staged(int idx, const i8l_config& c, const int8_t* a, int64_t 
     case 0: return launch_staged_t<128, 128, 64, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
     case 1: return launch_staged_t<256, 128, 64, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
     case 2: return launch_staged_t<128, 256, 64, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 3: return launch_staged_t<256, 256, 64, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 4: return launch_staged_t<256, 256, 128, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 5: return launch_staged_t<128, 128, 128, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 6: return launch_staged_t<256, 256, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 7: return launch_staged_t<256, 256, 128, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 8: return launch_staged_t<256, 128, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 9: return launch_staged_t<128, 256, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 10: return launch_staged_t<256, 128, 128, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
-    case 11: return launch_staged_t<128, 256, 128, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 3: return launch_staged_t<128, 128, 128, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 4: return launch_staged_t<256, 256, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 5: return launch_staged_t<256, 128, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 6: return launch_staged_t<128, 256, 64, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 7: return launch_staged_t<256, 128, 128, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 8: return launch_staged_t<128, 256, 128, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1255,16 +1448,16 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     c->stages = 1;
     return;
   }
-  // Prefill: direct-to-LDS macro tiles (the fastest measured family on MI355X).
+  // Prefill: direct-to-LDS macro tiles with the fragment reads overlapped with the MFMAs
+  // (the fastest measured family on MI355X): 256x256 tiles once there are enough of them,
+  // 128x128 tiles (more workgroups) below.
   c->group_m = 8;
   if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
-    *c = i8l_config{256, 256, 64, 8, 4, 8, 1};
-  } else if (N % 256 == 0 && K % 128 == 0) {
-    *c = i8l_config{128, 256, 128, 8, 3, 8, 1};
+    *c = i8l_config{256, 256, 64, 8, 12, 4, 1};
   } else if (N % 128 == 0 && K % 128 == 0) {
-    *c = i8l_config{128, 128, 128, 4, 4, 8, 1};
+    *c = i8l_config{128, 128, 128, 4, 12, 8, 1};
   } else if (N % 128 == 0 && K % 64 == 0) {
-    *c = i8l_config{128, 128, 64, 4, 4, 8, 1};
+    *c = i8l_config{128, 128, 64, 4, 12, 8, 1};
   } else {
     // narrow or odd shapes: the weight-streaming tile, one 128-token row block at a time
     int W = stream_max_threads(8, 1) / 64;
@@ -1297,7 +1490,8 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
               c.bm, c.bn, c.bk);
     return I8L_UNSUPPORTED;
   }
-  if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && !wlds_ok(c, K)) {
+  if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && dmap_index(c) < 0 &&
+      !wlds_ok(c, K)) {
     set_error("config %dx%dx%d w%d s%d g%d k%d is not built into this library", c.bm, c.bn,
               c.bk, c.warps, c.stages, c.group_m, c.split_k);
     return I8L_UNSUPPORTED;
@@ -1393,6 +1587,8 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     }
   } else if (c.stages == 2) {
     err = launch_staged(staged_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
+  } else if (c.stages >= 3 + kPipelined) {
+    err = launch_dmap(dmap_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   } else {
     err = launch_dma(dma_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   }

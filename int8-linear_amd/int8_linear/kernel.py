@@ -44,7 +44,10 @@ class Config:
     Prefill schedules (bm x bn macro tiles of 128 or 256, K in bk-byte steps, `group_m`
     rows of tiles walked together):
       stages == 2: double-buffered LDS staged through registers;
-      stages >= 3, bm >= 128: a ring of `stages` LDS buffers filled by direct-to-LDS loads.
+      3 <= stages <= 8, bm >= 128: a ring of `stages` LDS buffers filled by direct-to-LDS
+        loads;
+      stages >= 11: the same ring of stages - 8 buffers with the LDS fragment reads of each
+        MFMA substep overlapped with the MFMAs of the one before.
     A configuration the library was not built with raises NotSupported.
     """
 

@@ -31,16 +31,21 @@ ROTATE_BYTES = 512 << 20
 STREAM_TILES = [(1, 16), (2, 16), (4, 16), (8, 16), (1, 32), (2, 32), (4, 32), (1, 8), (2, 8),
                 (1, 4)]
 # (BM, BN, BK, waves) of the built staged tiles
-STAGED_TILES = [(128, 128, 64, 4), (256, 128, 64, 4), (128, 256, 64, 4), (256, 256, 64, 4),
-                (256, 256, 128, 4), (128, 128, 128, 4), (256, 256, 64, 8), (256, 256, 128, 8),
-                (256, 128, 64, 8), (128, 256, 64, 8), (256, 128, 128, 8), (128, 256, 128, 8)]
+STAGED_TILES = [(128, 128, 64, 4), (256, 128, 64, 4), (128, 256, 64, 4), (128, 128, 128, 4),
+                (256, 256, 64, 8), (256, 128, 64, 8), (128, 256, 64, 8), (256, 128, 128, 8),
+                (128, 256, 128, 8)]
 
 
 # (BM, BN, BK, waves, ring depth) of the built direct-to-LDS tiles
-DMA_TILES = [(256, 256, 64, 4, 3), (256, 256, 64, 4, 4), (256, 256, 64, 8, 3),
-             (256, 256, 64, 8, 4), (256, 128, 64, 8, 4), (128, 256, 64, 8, 4),
-             (256, 128, 128, 8, 3), (128, 256, 128, 8, 3), (128, 128, 128, 4, 4),
-             (128, 128, 64, 4, 4)]
+DMA_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 128, 64, 8, 4),
+             (128, 256, 64, 8, 4), (256, 128, 128, 8, 3), (128, 256, 128, 8, 3),
+             (128, 128, 128, 4, 4), (128, 128, 64, 4, 4), (256, 256, 64, 8, 5),
+             (256, 128, 64, 8, 6), (128, 256, 64, 8, 6), (128, 128, 64, 4, 8)]
+# the same with fragment reads overlapped with the MFMAs: stages = ring depth + 8
+PIPELINED = 8
+DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
+              (256, 128, 64, 8, 4), (128, 256, 64, 8, 4), (128, 256, 128, 8, 3),
+              (256, 128, 128, 8, 3), (128, 128, 64, 4, 4), (128, 128, 128, 4, 4)]
 
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
@@ -78,6 +83,11 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
         for bm, bn, bk, w, st in DMA_TILES:
             for g in (1, 8):
                 cfg = Config(bm, bn, bk, w, st, g)
+                if supported(m, n, k, cfg):
+                    out.append(cfg)
+        for bm, bn, bk, w, st in DMAP_TILES:
+            for g in (4, 8):
+                cfg = Config(bm, bn, bk, w, st + PIPELINED, g)
                 if supported(m, n, k, cfg):
                     out.append(cfg)
     return out

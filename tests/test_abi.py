@@ -64,7 +64,9 @@ def test_supported_decline_rule_matches_reference():
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 384, 4, 3, 1))  # K % (bk*warps)
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 512, 16, 3, 1))  # LDS > 160 KiB
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
-    assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 4, 2, 8))
+    assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 2, 8))
+    assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 4, 2, 8))  # would spill
+    assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 12, 8))  # overlapped ring
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 4, 8))   # DMA ring of 4
     assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 16, 2, 8))
 

@@ -60,13 +60,19 @@ TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64,
            Config(128, 16, 256, 4, 1, 1), Config(16, 32, 512, 8, 1, 1),
            Config(16, 8, 256, 4, 1, 1), Config(32, 8, 512, 8, 1, 1), Config(16, 4, 128, 2, 1, 1),
            Config(128, 128, 64, 4, 2, 8), Config(256, 128, 64, 4, 2, 1),
-           Config(128, 256, 64, 4, 2, 1), Config(256, 256, 64, 4, 2, 8),
-           Config(256, 256, 128, 4, 2, 8), Config(128, 128, 128, 4, 2, 1),
+           Config(128, 256, 64, 4, 2, 1), Config(128, 128, 128, 4, 2, 1),
            Config(256, 256, 64, 8, 2, 8), Config(256, 128, 64, 8, 2, 1),
            Config(128, 256, 128, 8, 2, 8),
-           Config(256, 256, 64, 4, 3, 8), Config(256, 256, 64, 8, 4, 8),
+           Config(256, 256, 64, 8, 3, 8), Config(256, 256, 64, 8, 4, 8),
+           Config(256, 256, 64, 8, 5, 4), Config(256, 128, 64, 8, 6, 8),
            Config(256, 128, 64, 8, 4, 1), Config(128, 256, 128, 8, 3, 8),
-           Config(128, 128, 64, 4, 4, 1)]
+           Config(128, 128, 64, 4, 4, 1), Config(128, 128, 64, 4, 8, 8),
+           # overlapped fragment reads (stages = ring depth + 8)
+           Config(256, 256, 64, 8, 11, 8), Config(256, 256, 64, 8, 12, 8),
+           Config(256, 256, 64, 8, 13, 4), Config(256, 128, 64, 8, 12, 8),
+           Config(128, 256, 64, 8, 12, 4), Config(128, 256, 128, 8, 11, 8),
+           Config(256, 128, 128, 8, 11, 8), Config(128, 128, 64, 4, 12, 1),
+           Config(128, 128, 128, 4, 12, 8)]
 
 
 @pytest.mark.parametrize("config", TILINGS, ids=lambda c: c.name.replace(" ", "_"))
