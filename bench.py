@@ -13,8 +13,12 @@ in the 256 MiB Infinity Cache.  `value` is the mean microseconds per linear over
 
 After the timed steps (not inside them): per-call graph-replay times of every sweep point,
 the roofline object of the dominant kernel (HIP events on the launch stream, algorithmic
-bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3), and the
-CPU baseline (the oracle's CPU restatement of the reference's path, on a bounded sample).
+bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3), the
+28-layer decoder stand-in in microseconds per layer (config 4), and the CPU baseline (the
+oracle's CPU restatement of the reference's path, on a bounded sample).
+
+    python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
+    python bench.py --only standin       # one extra section alone (quant|prefill|standin)
 Every GPU output is checked against a float64 reference before it is timed, after the
 output buffer has been poisoned.  Prints ONE JSON line.
 """
@@ -163,8 +167,20 @@ def roofline_config0(dev, launches: int = 0) -> dict:
             traffic = rec["bytes_per_launch"]
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": f"gemm_stream, config {cfg.name} (BASELINE config 0: M=16 K=2048 N=4096)",
+            "kernel": f"{schedule_of(cfg, k)}, config {cfg.name} "
+                      "(BASELINE config 0: M=16 K=2048 N=4096)",
             "bytes_per_launch": b0, "avg_launch_us": round(us, 3), "launches": reps}
+
+
+def schedule_of(cfg, k: int) -> str:
+    """The kernel a config launches (its name in a rocprofv3 kernel trace)."""
+    if cfg.stages == 1:
+        return "gemm_stream"
+    if cfg.stages == 2:
+        return "gemm_staged"
+    if cfg.stages == 3 and cfg.bm <= 32:
+        return "gemm_wlds1" if k == cfg.bk * cfg.warps else "gemm_wlds"
+    return "gemm_dmap" if cfg.stages >= 11 else "gemm_dma"
 
 
 def copy_calibration(dev, mib: int = 256) -> dict:
