@@ -1127,7 +1127,8 @@ struct WldsTile {
 };
 constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1, 8, 2},
                               {1, 8, 4},  {1, 8, 6},  {1, 8, 8},  {1, 4, 4},  {1, 4, 8},
-                              {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4}};
+                              {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4},  {4, 16, 2},
+                              {4, 16, 4}, {4, 8, 2},  {4, 8, 4},  {8, 16, 2}, {8, 8, 2}};
 constexpr size_t kMaxLds = 160 * 1024;
 
 size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
@@ -1137,7 +1138,7 @@ size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
 }
 
 bool wlds_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 3 || c.split_k != 1 || c.bm > 32 || c.warps < 1 || c.warps > 16) return false;
+  if (c.stages != 3 || c.split_k != 1 || c.bn > 16 || c.warps < 1 || c.warps > 16) return false;
   bool built = false;
   for (auto t : kWlds)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
@@ -1242,21 +1243,24 @@ template <int MT, int NC, int KS, int EK>
 hipError_t launch_wlds1_w(int W, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, hipStream_t st) {
   if constexpr (KS <= 8) {
-    if (W == 4 && (KS == 4 || KS == 8)) return launch_wlds1_k<MT, NC, KS, 4, EK>(a, lda, b, ldb, e, st);
+    if constexpr (MT <= 4)
+      if (W == 4 && (KS == 4 || KS == 8)) return launch_wlds1_k<MT, NC, KS, 4, EK>(a, lda, b, ldb, e, st);
     if (W == 8) return launch_wlds1_k<MT, NC, KS, 8, EK>(a, lda, b, ldb, e, st);
-    if (W == 16 && KS <= 6) return launch_wlds1_k<MT, NC, KS, 16, EK>(a, lda, b, ldb, e, st);
+    if constexpr (wlds_bound(MT, KS) >= 1024 && KS <= 6)
+      if (W == 16) return launch_wlds1_k<MT, NC, KS, 16, EK>(a, lda, b, ldb, e, st);
   }
   return hipErrorInvalidValue;
 }
 
-bool wlds1_built(int W, int ks) {
-  return (W == 4 && (ks == 4 || ks == 8)) || W == 8 || (W == 16 && ks <= 6);
+bool wlds1_built(int mt, int W, int ks) {
+  return (W == 4 && mt <= 4 && (ks == 4 || ks == 8)) || W == 8 ||
+         (W == 16 && ks <= 6 && wlds_bound(mt, ks) >= 1024);
 }
 
 template <int MT, int NC, int KS>
 hipError_t launch_wlds_t(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
-  if (K == (int64_t)c.bk * c.warps && wlds1_built(c.warps, KS)) {
+  if (K == (int64_t)c.bk * c.warps && wlds1_built(MT, c.warps, KS)) {
     switch (epi_kind(e)) {
       case EK_BF16: return launch_wlds1_w<MT, NC, KS, EK_BF16>(c.warps, a, lda, b, ldb, e, st);
       case EK_BF16_BBF16:
@@ -1280,6 +1284,8 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
   I8L_WLDS(1, 8, 2) I8L_WLDS(1, 8, 4) I8L_WLDS(1, 8, 6) I8L_WLDS(1, 8, 8)
   I8L_WLDS(1, 4, 4) I8L_WLDS(1, 4, 8)
   I8L_WLDS(2, 16, 2) I8L_WLDS(2, 16, 4) I8L_WLDS(2, 8, 2) I8L_WLDS(2, 8, 4)
+  I8L_WLDS(4, 16, 2) I8L_WLDS(4, 16, 4) I8L_WLDS(4, 8, 2) I8L_WLDS(4, 8, 4)
+  I8L_WLDS(8, 16, 2) I8L_WLDS(8, 8, 2)
 #undef I8L_WLDS
   return hipErrorInvalidValue;
 }
@@ -1575,7 +1581,7 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     err = hipGetLastError();
   } else if (c.stages == 1) {
     err = launch_stream(c, a, stride_am, b, stride_bn, e, (int)K, hs);
-  } else if (c.stages == 3 && c.bm <= 32) {
+  } else if (c.stages == 3 && c.bn <= 16) {
     // the schedule keeps in-tile row offsets in 32 bits
     if (stride_am > INT32_MAX / 32 || stride_bn > INT32_MAX / 16) {
       const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));

@@ -108,7 +108,7 @@ def test_weights_through_lds_schedule(tile, steps, waves):
     cfg = Config(16 * mt, nc, 64 * ks, waves, 3, 1)
     if not kernel.supported(16 * mt, n, k, cfg):
         pytest.skip(f"{cfg.name} is not built for K={k}")
-    for m in ((1, 5, 16) if mt == 1 else (17, 32)):
+    for m in {1: (1, 5, 16), 2: (17, 32), 4: (33, 64), 8: (65, 100, 128)}[mt]:
         say(f"w8a8_mm wlds m={m} k={k} n={n} config={cfg.name}")
         a, w = ints((m, k), 11 + m), ints((n, k), 12)
         one = torch.ones(1, device="cuda")
