@@ -184,9 +184,11 @@ __device__ __forceinline__ void store8(uint16_t* p, int e0, int n, const float* 
 
 // Max of non-negative values over the NW waves of a row: each wave's maximum goes through
 // LDS (sh holds kMaxWaves floats) and comes back as lanes 0..nw-1 of every wave of the row.
+// MULTI (nw > 1) is a compile-time choice, so a single-wave row has no branch here.
+template <bool MULTI>
 __device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float* sh) {
   v = wave_max(v);
-  if (nw == 1) return v;
+  if constexpr (!MULTI) return v;
   if (p.lane == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   return wave_max(p.lane < nw ? sh[p.slot * nw + p.lane] : 0.0f);
@@ -194,7 +196,7 @@ __device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float
 
 // The quantizer of a row whose values y (J chunks of 8 per lane) are final: absmax over the
 // row, scale and reciprocal, codes stored as 8-byte pieces, the scale by the row's first lane.
-template <int J, bool VEC>
+template <int J, bool VEC, bool MULTI>
 __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p, int n, int nw,
                                                int8_t* qrow, float* scale_out, int precise,
                                                float* sh) {
@@ -203,15 +205,14 @@ __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p
   for (int j = 0; j < J; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(y[j][i]));
-  const float absmax = row_max(am, p, nw, sh);
-  float scale, inv;
-  if (precise) {
-    scale = absmax / 127.0f;
-    inv = absmax == 0.0f ? 0.0f : 127.0f / absmax;
-  } else {
-    scale = absmax * (1.0f / 127.0f);
-    inv = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
-  }
+  const float absmax = row_max<MULTI>(am, p, nw, sh);
+  // both division conventions, selected (once per row: no branch on the path)
+  const float s_div = absmax / 127.0f;
+  const float i_div = absmax == 0.0f ? 0.0f : 127.0f / absmax;
+  const float s_rcp = absmax * (1.0f / 127.0f);
+  const float i_rcp = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
+  const float scale = precise ? s_div : s_rcp;
+  const float inv = precise ? i_div : i_rcp;
   if (p.rw == 0 && p.lane == 0) *scale_out = scale;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -240,7 +241,7 @@ __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p
 // ------------------------------------------------------------------ add + RMSNorm + quant
 // J and NW are powers of two, so each wave covers an aligned power-of-two span of the row
 // and the wave/chunk/lane reductions together evaluate the padded row's pairwise tree.
-template <int J, int DT, int WDT, bool VEC>
+template <int J, int DT, int WDT, bool VEC, bool RES, bool MULTI>
 __global__ void __launch_bounds__(1024)
 add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
                          const uint16_t* __restrict__ w, float eps, int8_t* __restrict__ q,
@@ -254,7 +255,7 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   float xv[J][8];
 #pragma unroll
   for (int j = 0; j < J; ++j) load8<DT, VEC>(x + ro, chunk_base<J>(p, j), H, xv[j]);
-  if (res) {
+  if constexpr (RES) {
     float rv[J][8];
 #pragma unroll
     for (int j = 0; j < J; ++j) load8<DT, VEC>(res + ro, chunk_base<J>(p, j), H, rv[j]);
@@ -283,7 +284,7 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 #pragma unroll
     for (int j = 0; j < J; j += 2 * st) node[j] = node[j] + node[j + st];
   double tot = node[0];
-  if (nw > 1) {
+  if constexpr (MULTI) {
     // the nw wave nodes (aligned, a power of two of them) become lanes 0..nw-1 of a tree
     // whose other leaves are +0, which leaves every sum unchanged
     if (p.lane == 0) dsh[threadIdx.x >> 6] = tot;
@@ -307,11 +308,11 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
       xv[j][i + 1] = b;
     }
   }
-  quantize_store<J, VEC>(xv, p, H, nw, q + ro, scale + p.row, precise, fsh);
+  quantize_store<J, VEC, MULTI>(xv, p, H, nw, q + ro, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ SiLU-and-mul + quant
-template <int J, int DT, bool VEC, bool ROUND>
+template <int J, int DT, bool VEC, bool ROUND, bool MULTI>
 __global__ void __launch_bounds__(1024)
 silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
                       float* __restrict__ scale, int64_t M, int I, int nw, int rpb,
@@ -382,11 +383,11 @@ silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
         y[j][2 * i + 1] = a[1];
       }
   }
-  quantize_store<J, VEC>(y, p, I, nw, q + p.row * I, scale + p.row, precise, fsh);
+  quantize_store<J, VEC, MULTI>(y, p, I, nw, q + p.row * I, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ plain per-token quant
-template <int J, int DT, bool VEC>
+template <int J, int DT, bool VEC, bool MULTI>
 __global__ void __launch_bounds__(1024)
 quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
              float* __restrict__ scale, int64_t M, int H, int nw, int rpb, int precise) {
@@ -396,7 +397,7 @@ quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q
   float y[J][8];
 #pragma unroll
   for (int j = 0; j < J; ++j) load8<DT, VEC>(x + p.row * ldx, chunk_base<J>(p, j), H, y[j]);
-  quantize_store<J, VEC>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
+  quantize_store<J, VEC, MULTI>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -458,14 +459,15 @@ Geom flat_geom(int64_t M, int n, bool vec) {
 dim3 grid_of(int64_t M, const Geom& g) { return dim3((unsigned)((M + g.rpb - 1) / g.rpb)); }
 dim3 block_of(const Geom& g) { return dim3(64 * g.nw * g.rpb); }
 
-// Kernel selection: the element path (VEC false) is built for J = 4 only.
-template <int DT, int WDT>
-void launch_norm(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
-                 const uint16_t* res, const uint16_t* w, float eps, int8_t* q, float* scale,
-                 uint16_t* rout, int64_t M, int H, int precise) {
+// Kernel selection: the element path (VEC false) is built for J = 4 only.  The residual and
+// the multi-wave row are compile-time choices of the kernel, not branches inside it.
+template <int DT, int WDT, bool RES, bool MULTI>
+void launch_norm_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                   const uint16_t* res, const uint16_t* w, float eps, int8_t* q, float* scale,
+                   uint16_t* rout, int64_t M, int H, int precise) {
 #define I8L_NORM(J_, V_)                                                                    \
-  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<J_, DT, WDT, V_>), grid, block_of(g), 0, st, x, \
-                     res, w, eps, q, scale, rout, M, H, g.nw, g.rpb, precise)
+  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<J_, DT, WDT, V_, RES, MULTI>), grid, block_of(g), \
+                     0, st, x, res, w, eps, q, scale, rout, M, H, g.nw, g.rpb, precise)
   if (!vec) I8L_NORM(4, false);
   else if (g.j == 1) I8L_NORM(1, true);
   else if (g.j == 2) I8L_NORM(2, true);
@@ -473,12 +475,25 @@ void launch_norm(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint1
 #undef I8L_NORM
 }
 
-template <int DT, bool ROUND>
-void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* gu,
-                 int8_t* q, float* scale, int64_t M, int I, int precise) {
+template <int DT, int WDT>
+void launch_norm(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                 const uint16_t* res, const uint16_t* w, float eps, int8_t* q, float* scale,
+                 uint16_t* rout, int64_t M, int H, int precise) {
+  const bool multi = g.nw > 1;
+  if (res)
+    multi ? launch_norm_k<DT, WDT, true, true>(g, vec, grid, st, x, res, w, eps, q, scale, rout, M, H, precise)
+          : launch_norm_k<DT, WDT, true, false>(g, vec, grid, st, x, res, w, eps, q, scale, rout, M, H, precise);
+  else
+    multi ? launch_norm_k<DT, WDT, false, true>(g, vec, grid, st, x, res, w, eps, q, scale, rout, M, H, precise)
+          : launch_norm_k<DT, WDT, false, false>(g, vec, grid, st, x, res, w, eps, q, scale, rout, M, H, precise);
+}
+
+template <int DT, bool ROUND, bool MULTI>
+void launch_silu_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* gu,
+                   int8_t* q, float* scale, int64_t M, int I, int precise) {
 #define I8L_SILU(J_, V_)                                                                    \
-  hipLaunchKernelGGL((silu_mul_quant_kernel<J_, DT, V_, ROUND>), grid, block_of(g), 0, st, gu, \
-                     q, scale, M, I, g.nw, g.rpb, precise)
+  hipLaunchKernelGGL((silu_mul_quant_kernel<J_, DT, V_, ROUND, MULTI>), grid, block_of(g), 0, \
+                     st, gu, q, scale, M, I, g.nw, g.rpb, precise)
   if (!vec) I8L_SILU(4, false);
   else if (g.j == 1) I8L_SILU(1, true);
   else if (g.j == 2) I8L_SILU(2, true);
@@ -487,18 +502,36 @@ void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint1
 #undef I8L_SILU
 }
 
-template <int DT>
-void launch_quant(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
-                  int64_t ldx, int8_t* q, float* scale, int64_t M, int H, int precise) {
+template <int DT, bool ROUND>
+void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* gu,
+                 int8_t* q, float* scale, int64_t M, int I, int precise) {
+  if (g.nw > 1)
+    launch_silu_k<DT, ROUND, true>(g, vec, grid, st, gu, q, scale, M, I, precise);
+  else
+    launch_silu_k<DT, ROUND, false>(g, vec, grid, st, gu, q, scale, M, I, precise);
+}
+
+template <int DT, bool MULTI>
+void launch_quant_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                    int64_t ldx, int8_t* q, float* scale, int64_t M, int H, int precise) {
 #define I8L_QUANT(J_, V_)                                                                   \
-  hipLaunchKernelGGL((quant_kernel<J_, DT, V_>), grid, block_of(g), 0, st, x, ldx, q, scale, \
-                     M, H, g.nw, g.rpb, precise)
+  hipLaunchKernelGGL((quant_kernel<J_, DT, V_, MULTI>), grid, block_of(g), 0, st, x, ldx, q, \
+                     scale, M, H, g.nw, g.rpb, precise)
   if (!vec) I8L_QUANT(4, false);
   else if (g.j == 1) I8L_QUANT(1, true);
   else if (g.j == 2) I8L_QUANT(2, true);
   else if (g.j == 3) I8L_QUANT(3, true);
   else I8L_QUANT(4, true);
 #undef I8L_QUANT
+}
+
+template <int DT>
+void launch_quant(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
+                  int64_t ldx, int8_t* q, float* scale, int64_t M, int H, int precise) {
+  if (g.nw > 1)
+    launch_quant_k<DT, true>(g, vec, grid, st, x, ldx, q, scale, M, H, precise);
+  else
+    launch_quant_k<DT, false>(g, vec, grid, st, x, ldx, q, scale, M, H, precise);
 }
 
 }  // namespace
