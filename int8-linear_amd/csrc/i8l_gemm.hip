@@ -1154,7 +1154,8 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {256, 256, 64, 2, 4, 5}, {256, 128, 64, 2, 4, 4},
                              {128, 256, 64, 2, 4, 4}, {128, 256, 128, 2, 4, 3},
                              {256, 128, 128, 2, 4, 3}, {128, 128, 64, 2, 2, 4},
-                             {128, 128, 128, 2, 2, 4}};
+                             {128, 128, 128, 2, 2, 4}, {64, 128, 128, 2, 2, 4},
+                             {64, 256, 128, 2, 4, 3}, {64, 128, 64, 2, 2, 6}};
 constexpr int kPipelined = 8;
 
 int dmap_index(const i8l_config& c) {
@@ -1389,6 +1390,9 @@ hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t ld
     case 6: return launch_dmap_t<256, 128, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
     case 7: return launch_dmap_t<128, 128, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 8: return launch_dmap_t<128, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 9: return launch_dmap_t<64, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 10: return launch_dmap_t<64, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 11: return launch_dmap_t<64, 128, 64, 2, 2, 6>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1441,6 +1445,12 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
         return;
       }
     }
+  }
+  // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
+  // direct-to-LDS ring; the activations are re-read N/128 times instead of N/16 or N/32.
+  if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 32 && N >= 6144))) {
+    *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
+    return;
   }
   if (M <= 128) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;

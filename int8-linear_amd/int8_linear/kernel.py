@@ -41,7 +41,7 @@ class Config:
         steps, so bk == 64 * warps.
       stages == 3, bm <= 32: weights copied through LDS with direct-to-LDS loads; each of the
         `warps` waves owns one K slice taken bk bytes per step (K a multiple of bk * warps).
-    Prefill schedules (bm x bn macro tiles of 128 or 256, K in bk-byte steps, `group_m`
+    Prefill schedules (bm x bn macro tiles of 64 to 256, K in bk-byte steps, `group_m`
     rows of tiles walked together):
       stages == 2: double-buffered LDS staged through registers;
       3 <= stages <= 8, bm >= 128: a ring of `stages` LDS buffers filled by direct-to-LDS
@@ -77,8 +77,9 @@ def _cconfig(cfg: Config) -> _lib.CConfig:
 
 
 def default_config(m: int, n: int, k: int) -> Config:
-    """The untuned choice: the weight-streaming decode schedule up to 128 tokens, staged
-    macro tiles above (the library's own rule, i8l_default_config)."""
+    """The untuned choice (the library's own rule, i8l_default_config): weights through LDS
+    up to 32 tokens, 64x128 overlapped-ring tiles for wide N up to 128 tokens and for any N
+    up to 512, weight streaming otherwise up to 128 tokens, prefill macro tiles above."""
     c = _lib.CConfig()
     _lib.check(_lib.lib().i8l_default_config(m, n, k, c), NotSupported)
     return Config(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, c.split_k)

@@ -45,7 +45,8 @@ DMA_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 128, 64, 8, 4),
 PIPELINED = 8
 DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
               (256, 128, 64, 8, 4), (128, 256, 64, 8, 4), (128, 256, 128, 8, 3),
-              (256, 128, 128, 8, 3), (128, 128, 64, 4, 4), (128, 128, 128, 4, 4)]
+              (256, 128, 128, 8, 3), (128, 128, 64, 4, 4), (128, 128, 128, 4, 4),
+              (64, 128, 128, 4, 4), (64, 256, 128, 8, 3), (64, 128, 64, 4, 6)]
 
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
@@ -75,7 +76,7 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
                 cfg = Config(16 * mt, bn, 64 * w, w, 1, 1)
                 if supported(m, n, k, cfg):
                     out.append(cfg)
-    if m >= 64:
+    if m >= 33:
         for bm, bn, bk, w in STAGED_TILES:
             for g in (1, 8):
                 cfg = Config(bm, bn, bk, w, 2, g)

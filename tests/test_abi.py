@@ -50,6 +50,10 @@ def test_default_config_regimes():
     p = default_config(4096, 28672, 4096)
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
     assert default_config(300, 2048, 2048).stages >= 2
+    mid = default_config(96, 12288, 2048)                   # 64-token overlapped-ring tiles
+    assert (mid.bm, mid.bn, mid.stages) == (64, 128, 12)
+    assert default_config(400, 2048, 6144).bm == 64
+    assert default_config(96, 4096, 2048).stages == 1       # narrower N keeps streaming
     for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
         assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
 
