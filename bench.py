@@ -18,7 +18,7 @@ bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3
 oracle's CPU restatement of the reference's path, on a bounded sample).
 
     python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
-    python bench.py --only standin       # one extra section alone (quant|prefill|standin)
+    python bench.py --only standin       # one extra section alone (quant|prefill|standin|launch)
 Every GPU output is checked against a float64 reference before it is timed, after the
 output buffer has been poisoned.  Prints ONE JSON line.
 """
@@ -228,7 +228,7 @@ def main() -> int:
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
-    ap.add_argument("--only", choices=["quant", "prefill", "standin"], default=None,
+    ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch"], default=None,
                     help="run one extra section alone (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -249,7 +249,8 @@ def main() -> int:
         print(json.dumps({"roofline": rf, "calibration": cal}), flush=True)
         return 0
     if args.only:
-        fn = {"quant": bench_quant, "prefill": bench_prefill, "standin": bench_standin}[args.only]
+        fn = {"quant": bench_quant, "prefill": bench_prefill, "standin": bench_standin,
+              "launch": bench_launch}[args.only]
         print(json.dumps({args.only: fn(dev)}), flush=True)
         return 0
     shapes = SHAPES["qwen3-1.7b-vllm"]
@@ -326,6 +327,7 @@ def main() -> int:
         result["quant"] = bench_quant(dev)
         result["prefill"] = bench_prefill(dev)
         result["standin"] = bench_standin(dev)
+        result["launch"] = bench_launch(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -377,6 +379,137 @@ def bench_standin(dev) -> dict:
             "layers": standin.LAYERS, "weight_bytes_per_layer": int(wbytes),
             "step": "add_rmsnorm_quant > qkv > quant(q cols) > o > add_rmsnorm_quant > gate_up "
                     "> silu_mul_quant > down, one HIP graph per 28-layer step"}
+
+
+LAUNCH_SHAPES = [("q_proj, o_proj", 2048, 2048), ("gate_up_proj", 2048, 12288)]
+LAUNCH_M = [1, 4, 16]
+
+
+def time_host_us(fn, iters: int, windows: int) -> list[float]:
+    """CPU microseconds per call, nothing synchronized inside a window (the host cost)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(windows):
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        out.append((time.perf_counter() - t0) / iters * 1e6)
+        torch.cuda.synchronize()
+    return out
+
+
+def time_eager_us(fn, iters: int, windows: int) -> list[float]:
+    """Microseconds per call between HIP events around `iters` back-to-back eager calls."""
+    import torch
+    out = []
+    for _ in range(windows):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b) * 1e3 / iters)
+    return out
+
+
+class _ctypes_only:
+    """Inside: the Python wrappers launch through ctypes (the C++ binding is set aside)."""
+
+    def __enter__(self):
+        from int8_linear import _lib
+        self.saved = _lib.fast()
+        _lib._fast_mod = None
+
+    def __exit__(self, *exc):
+        from int8_linear import _lib
+        _lib._fast_mod = self.saved
+
+
+def bench_launch(dev, iters: int = 300, windows: int = 5) -> dict:
+    """Host cost of one eager call (the reference's bench/launch_overhead.py:52-153 on the
+    same shapes and batch sizes): CPU time per call, back-to-back time between HIP events
+    (a step without graphs), and graph replay (the GPU work alone), per launch path."""
+    import torch
+    import torch.nn.functional as F
+
+    from int8_linear import fused_quant as fq
+    from int8_linear import vllm_patch
+    from int8_linear.kernel import w8a8_mm
+    from int8_linear.operands import operands, seed_of
+
+    def ctypes_path(fn):
+        def run():
+            with _ctypes_only():
+                return fn()
+        return run
+
+    rows = []
+    for label, k, n in LAUNCH_SHAPES:
+        for m in LAUNCH_M:
+            d = operands(m, k, n, seed_of(m, k, n), device=dev)
+            a, wb = d["a"], d["w"]
+            q = (d["a_q"], d["w_qt"], d["a_s"], d["w_s"], torch.bfloat16, None)
+            provs = [
+                ("bf16 F.linear (torch, hipBLASLt)", lambda: F.linear(a, wb)),
+                ("int8 torch._int_mm (hipBLASLt, int32 out, no scales)",
+                 lambda: torch._int_mm(d["a_q"], d["w_qt"])),
+                ("ours, ctypes", ctypes_path(lambda: w8a8_mm(*q))),
+                ("ours, C++ binding", lambda: w8a8_mm(*q)),
+                ("ours, custom op", lambda: torch.ops.int8_linear.w8a8_mm(*q)),
+                ("ours, vLLM entry", lambda: vllm_patch.scaled_mm(*q)),
+            ]
+            ref = None
+            for name, fn in provs:
+                row = {"shape": label, "k": k, "n": n, "m": m, "provider": name}
+                try:
+                    out = fn()
+                    torch.cuda.synchronize()
+                except Exception as e:  # a vendor path that does not take this shape
+                    row["status"] = f"{type(e).__name__}: {str(e).splitlines()[0][:80]}"
+                    rows.append(row)
+                    continue
+                if name.startswith("ours"):
+                    ref = out if ref is None else ref
+                    if not torch.equal(out, ref):
+                        raise SystemExit(f"FAIL launch paths differ: {name} {label} M={m}")
+                h = time_host_us(fn, iters, windows)
+                e = time_eager_us(fn, iters, windows)
+                try:
+                    g = graph_time_us(lambda i: fn(), 100, windows)
+                except Exception as ex:
+                    g = None
+                    row["graph_status"] = type(ex).__name__
+                row.update(status="ok", host_us=round(statistics.median(h), 2),
+                           eager_us=round(statistics.median(e), 2),
+                           graph_us=round(g, 2) if g is not None else None)
+                rows.append(row)
+                log(f"launch {label} M={m} {name}: host {row['host_us']} eager "
+                    f"{row['eager_us']} graph {row['graph_us']} us")
+    # the fused quantizers of one decode token row set, ctypes vs the binding
+    for m in LAUNCH_M:
+        x = torch.randn((m, 2048), device=dev).to(torch.bfloat16)
+        r = torch.randn((m, 2048), device=dev).to(torch.bfloat16)
+        w = torch.ones(2048, device=dev, dtype=torch.bfloat16)
+        gu = torch.randn((m, 12288), device=dev).to(torch.bfloat16)
+        ops = [("add_rmsnorm_quant", lambda: fq.add_rmsnorm_quant(x, r, w, 1e-6)),
+               ("silu_mul_quant", lambda: fq.silu_mul_quant(gu))]
+        for opname, fn in ops:
+            for name, f in (("ours, ctypes", ctypes_path(fn)), ("ours, C++ binding", fn)):
+                h = time_host_us(f, iters, windows)
+                e = time_eager_us(f, iters, windows)
+                g = graph_time_us(lambda i: f(), 100, windows)
+                rows.append({"shape": opname, "k": 2048, "n": 2048 if opname[0] == "a" else 6144,
+                             "m": m, "provider": name, "status": "ok",
+                             "host_us": round(statistics.median(h), 2),
+                             "eager_us": round(statistics.median(e), 2), "graph_us": round(g, 2)})
+                log(f"launch {opname} M={m} {name}: host {rows[-1]['host_us']} eager "
+                    f"{rows[-1]['eager_us']} graph {rows[-1]['graph_us']} us")
+    cols = ["shape", "m", "provider", "host_us", "eager_us", "graph_us"]
+    return {"cols": cols, "rows": [[r.get(c, r.get("status")) for c in cols] for r in rows],
+            "iters": iters, "windows": windows}
 
 
 def bench_prefill(dev) -> dict:

@@ -176,6 +176,15 @@ __device__ __forceinline__ v4i ld16_stream(const int8_t* p) {
   return __builtin_nontemporal_load((const v4i*)p);
 }
 
+// Column tile of a decode workgroup.  The dispatcher deals workgroups to the 8 XCDs
+// round-robin by linear id; with a multiple of 8 column tiles per row, XCD x is given the
+// contiguous column range [x, x+1) * gridDim.x/8, so the output lines (and the L2 lines
+// they are assembled in) are written from one XCD rather than in pieces from eight.
+__device__ __forceinline__ int64_t xcd_col_tile() {
+  const int gx = gridDim.x, bx = blockIdx.x;
+  return gx % 8 == 0 ? (int64_t)(bx % 8) * (gx / 8) + bx / 8 : (int64_t)bx;
+}
+
 // ------------------------------------------------------------------ stream schedule
 // Workgroup = W waves on the same 16*NT output columns and 16*MT tokens; wave w owns the
 // contiguous K slice [w*ks*64, (w+1)*ks*64).  Lane l of a wave loads, per 64-byte K step,
@@ -201,7 +210,7 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   const int wave = threadIdx.x >> 6;
   const int W = blockDim.x >> 6;
   const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * (NC * NT);
+  const int64_t n0 = xcd_col_tile() * (NC * NT);
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
   const int64_t kbeg = (int64_t)wave * ks * 64 + grp * 16;
 
@@ -321,6 +330,11 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // With NC < 16, MFMA rows i and i+NC read the same weight row and only rows below NC are
 // stored.  Token rows past M read row 0 and are never stored.
 __host__ __device__ constexpr int wlds_bound(int mt, int ks) { return mt * ks <= 6 ? 1024 : 512; }
+// Whether the multi-step kernel's registers fit: two sets of activation fragments, the
+// weight fragments of a step and the accumulators, in VGPRs (64 x 4 bytes each).
+__host__ __device__ constexpr bool wlds_multi_fits(int mt, int nc, int ks) {
+  return 8 * ks * mt + 4 * ks * (nc > 16 ? nc / 16 : 1) + 4 * mt * (nc > 16 ? nc / 16 : 1) <= 176;
+}
 
 // s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
 // no LDS read of the DMA'd data is scheduled above the wait.
@@ -348,6 +362,10 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   constexpr int NI = SB / 1024;              // DMA instructions per wave per step
   static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
   constexpr int AL = MT * KS;                // activation loads per lane per step
+  constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
+  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int FR = MT * NF;                // output fragments, numbered i * NF + f
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
@@ -356,14 +374,14 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * NC;
+  const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
   const int64_t kw = (int64_t)wave * steps * S;
   int8_t* wbuf = lds + (size_t)wave * nbuf * SB;
 
   // DMA sources of this lane: instruction t writes LDS bytes [t*1024, t*1024+1024) of the
   // step buffer, lane l the 16 bytes at +16*l, which is row o / S, slot (o % S) / 16.
-  // Rows of a tile are < 16 apart, so their offsets fit 32 bits.
+  // Rows of a tile are < 32 apart, so their offsets fit 32 bits.
   const int8_t* Bw = B + n0 * ldb + kw;
   const int ldb32 = (int)ldb;
   const int8_t* gsrc[NI];
@@ -382,15 +400,20 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     const int ml = 16 * i + r16;
     ap[i] = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
   }
-  // MFMA-layout read offsets of one step: row br, chunk 4s + grp
-  const int br = r16 % NC;
-  int rofs[KS];
+  // MFMA-layout read offsets of one step: fragment f's row br, chunk 4s + grp
+  int rofs[KS][NF];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) rofs[s] = br * S + 16 * ((4 * s + grp) ^ (br & SWM));
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) rofs[s][f] = br * S + 16 * ((4 * s + grp) ^ (br & SWM));
+  }
 
-  v4i acc[MT];
+  v4i acc[MT][NF];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = v4i{0, 0, 0, 0};
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
 
   v4i a0[KS][MT], a1[KS][MT];
   // `fenced`: nothing of the previous step's MFMA work moves below the start of the issue,
@@ -412,24 +435,28 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   };
   auto compute = [&](const v4i (&aa)[KS][MT], int step) {
     const int8_t* base = wbuf + (step % nbuf) * SB;
-    v4i b[KS];
+    v4i b[KS][NF];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) b[s] = *(const v4i*)(base + rofs[s]);
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) b[s][f] = *(const v4i*)(base + rofs[s][f]);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int i = 0; i < MT; ++i)
-        acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s], aa[s][i], acc[i], 0, 0, 0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], aa[s][i], acc[i][f], 0, 0, 0);
   };
 
   issue(a0, 0, steps > 1);
-  // The wave that stores fragment f (f % W == wave) loads its epilogue operands now, behind
-  // the first step, so their latency hides under the main loop.
+  // The wave that stores fragment fr (fr % W == wave) loads its epilogue operands now,
+  // behind the first step, so their latency hides under the main loop.
   Cols4 cl0;
   float sa0 = 0.0f;
-  if (wave < MT && 4 * grp < NC) {
-    const int64_t m = m0 + 16 * wave + r16;
-    cl0 = load_cols4<EK>(e, n0 + 4 * grp);
+  if (wave < FR && 4 * grp < NCF) {
+    const int64_t m = m0 + 16 * (wave / NF) + r16;
+    cl0 = load_cols4<EK>(e, n0 + NCF * (wave % NF) + 4 * grp);
     sa0 = load_sa<EK>(e, m < e.M ? m : 0);
   }
   // Steady state: every step's loads are issued before the wait for the previous step, and
@@ -456,29 +483,34 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   }
 
   // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
-  v4i* red = (v4i*)(lds + (size_t)W * nbuf * SB);  // [W][MT][64]
+  v4i* red = (v4i*)(lds + (size_t)W * nbuf * SB);  // [W][FR][64]
   if (W > 1) {
 #pragma unroll
-    for (int f = 0; f < MT; ++f) red[(wave * MT + f) * 64 + lane] = acc[f];
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) red[(wave * FR + q * NF + f) * 64 + lane] = acc[q][f];
     __syncthreads();
   }
-  for (int f = wave; f < MT; f += W) {
+  for (int fr = wave; fr < FR; fr += W) {
     v4i sum;
     if (W > 1) {
-      sum = red[f * 64 + lane];
-      for (int w = 1; w < W; ++w) sum += red[(w * MT + f) * 64 + lane];
+      sum = red[fr * 64 + lane];
+      for (int w = 1; w < W; ++w) sum += red[(w * FR + fr) * 64 + lane];
     } else {
-      sum = acc[0];
+      sum = acc[0][0];
 #pragma unroll
-      for (int q = 1; q < MT; ++q)
-        if (q == f) sum = acc[q];
+      for (int q = 0; q < MT; ++q)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          if (q * NF + f == fr) sum = acc[q][f];
     }
-    const int64_t m = m0 + 16 * f + r16;
-    if (m < e.M && 4 * grp < NC) {
-      if (f == wave)
-        store4s<EK>(e, m, n0 + 4 * grp, sum, cl0, sa0);
+    const int64_t m = m0 + 16 * (fr / NF) + r16;
+    const int64_t n = n0 + NCF * (fr % NF) + 4 * grp;
+    if (m < e.M && 4 * grp < NCF) {
+      if (fr == wave)
+        store4s<EK>(e, m, n, sum, cl0, sa0);
       else
-        store4<EK>(e, m, n0 + 4 * grp, sum);
+        store4<EK>(e, m, n, sum);
     }
   }
 }
@@ -499,13 +531,17 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
   constexpr int SB = NC * S;
   constexpr int NI = SB / 1024;
   static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
-  static_assert(MT <= W, "every fragment needs a storing wave");
+  constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
+  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int FR = MT * NF;                // output fragments of the tile
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  static_assert(FR <= W, "every fragment needs a storing wave");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, grp = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * NC;
+  const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
   const int64_t kw = (int64_t)wave * S;
   int8_t* wbuf = lds + (size_t)wave * SB;
@@ -530,40 +566,51 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
 #pragma unroll
     for (int s = 0; s < KS; ++s) a[s][i] = ld16(ap + 64 * s);
   }
-  // Epilogue operands of the fragment this wave stores (waves below MT), loaded behind the
-  // tile; lanes past NC columns load a valid neighbour and never store.
+  // Wave w < FR stores fragment (token block w / NF, column block w % NF) and loads its
+  // epilogue operands now, behind the tile; lanes past NCF columns load a valid neighbour
+  // and never store.
   Cols4 cl;
   float sam = 0.0f;
-  const int64_t mrow = m0 + 16 * wave + r16;
-  const int64_t ncol = n0 + 4 * (grp & (NC / 4 - 1));
-  if (wave < MT) {
+  const int64_t mrow = m0 + 16 * (wave / NF) + r16;
+  const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+  if (wave < FR) {
     cl = load_cols4<EK>(e, ncol);
     sam = load_sa<EK>(e, mrow < e.M ? mrow : m0);
   }
   wait_vmcnt_wlds<0>();
-  const int br = r16 % NC;
-  v4i b[KS];
+  v4i b[KS][NF];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) b[s] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
-  v4i acc[MT];
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = v4i{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s)
+      b[s][f] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+  }
+  v4i acc[MT][NF];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int i = 0; i < MT; ++i)
-      acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s], a[s][i], acc[i], 0, 0, 0);
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s][i], acc[i][f], 0, 0, 0);
 
   // cross-wave sum (exact int32), then the storing waves apply the epilogue
-  v4i* red = (v4i*)(lds + (size_t)W * SB);  // [W][MT][64]
+  v4i* red = (v4i*)(lds + (size_t)W * SB);  // [W][FR][64]
 #pragma unroll
-  for (int f = 0; f < MT; ++f) red[(wave * MT + f) * 64 + lane] = acc[f];
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) red[(wave * FR + i * NF + f) * 64 + lane] = acc[i][f];
   __syncthreads();
-  if (wave < MT) {
+  if (wave < FR) {
     v4i sum = red[wave * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < W; ++w) sum += red[(w * MT + wave) * 64 + lane];
-    if (mrow < e.M && 4 * grp < NC) store4s<EK>(e, mrow, ncol, sum, cl, sam);
+    for (int w = 1; w < W; ++w) sum += red[(w * FR + wave) * 64 + lane];
+    if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
   }
 }
 
@@ -1128,23 +1175,31 @@ struct WldsTile {
 constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1, 8, 2},
                               {1, 8, 4},  {1, 8, 6},  {1, 8, 8},  {1, 4, 4},  {1, 4, 8},
                               {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4},  {4, 16, 2},
-                              {4, 16, 4}, {4, 8, 2},  {4, 8, 4},  {8, 16, 2}, {8, 8, 2}};
+                              {4, 16, 4}, {4, 8, 2},  {4, 8, 4},  {8, 16, 2}, {8, 8, 2},
+                              {1, 32, 2}, {1, 32, 4}, {2, 32, 2}, {2, 32, 4}, {4, 32, 2},
+                              {4, 32, 4}};
 constexpr size_t kMaxLds = 160 * 1024;
 
 size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
   const int64_t steps = K / ((int64_t)c.bk * c.warps);
   const int nbuf = steps > 1 ? 2 : 1;
-  return (size_t)c.warps * nbuf * c.bn * c.bk + (size_t)c.warps * (c.bm / 16) * 1024;
+  const int nf = c.bn > 16 ? c.bn / 16 : 1;  // 16-column fragments a wave reduces
+  return (size_t)c.warps * nbuf * c.bn * c.bk + (size_t)c.warps * (c.bm / 16) * nf * 1024;
 }
 
+bool wlds1_built(int mt, int nc, int W, int ks);
+
 bool wlds_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 3 || c.split_k != 1 || c.bn > 16 || c.warps < 1 || c.warps > 16) return false;
+  if (c.stages != 3 || c.split_k != 1 || c.bn > 32 || c.warps < 1 || c.warps > 16) return false;
   bool built = false;
   for (auto t : kWlds)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
         c.warps * 64 <= wlds_bound(t.mt, t.ks))
       built = true;
   if (!built || K <= 0 || K % ((int64_t)c.bk * c.warps)) return false;
+  const bool one_step = K == (int64_t)c.bk * c.warps &&
+                        wlds1_built(c.bm / 16, c.bn, c.warps, c.bk / 64);
+  if (!one_step && !wlds_multi_fits(c.bm / 16, c.bn, c.bk / 64)) return false;
   return wlds_lds_bytes(c, K) <= kMaxLds;
 }
 
@@ -1226,7 +1281,7 @@ template <int MT, int NC, int KS, int W, int EK>
 hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, hipStream_t st) {
   auto kern = gemm_wlds1<MT, NC, KS, W, EK>;
-  const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * 1024;
+  const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * (NC > 16 ? NC / 16 : 1) * 1024;
   static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
   if (!attr_set && shm > 64 * 1024) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1243,25 +1298,28 @@ hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t
 template <int MT, int NC, int KS, int EK>
 hipError_t launch_wlds1_w(int W, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, hipStream_t st) {
+  constexpr int FR = MT * (NC > 16 ? NC / 16 : 1);  // fragments: one storing wave each
   if constexpr (KS <= 8) {
-    if constexpr (MT <= 4)
+    if constexpr (FR <= 4)
       if (W == 4 && (KS == 4 || KS == 8)) return launch_wlds1_k<MT, NC, KS, 4, EK>(a, lda, b, ldb, e, st);
-    if (W == 8) return launch_wlds1_k<MT, NC, KS, 8, EK>(a, lda, b, ldb, e, st);
+    if constexpr (FR <= 8)
+      if (W == 8) return launch_wlds1_k<MT, NC, KS, 8, EK>(a, lda, b, ldb, e, st);
     if constexpr (wlds_bound(MT, KS) >= 1024 && KS <= 6)
       if (W == 16) return launch_wlds1_k<MT, NC, KS, 16, EK>(a, lda, b, ldb, e, st);
   }
   return hipErrorInvalidValue;
 }
 
-bool wlds1_built(int mt, int W, int ks) {
-  return (W == 4 && mt <= 4 && (ks == 4 || ks == 8)) || W == 8 ||
-         (W == 16 && ks <= 6 && wlds_bound(mt, ks) >= 1024);
+bool wlds1_built(int mt, int nc, int W, int ks) {
+  const int fr = mt * (nc > 16 ? nc / 16 : 1);
+  return ks <= 8 && ((W == 4 && fr <= 4 && (ks == 4 || ks == 8)) || (W == 8 && fr <= 8) ||
+                     (W == 16 && ks <= 6 && wlds_bound(mt, ks) >= 1024));
 }
 
 template <int MT, int NC, int KS>
 hipError_t launch_wlds_t(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
-  if (K == (int64_t)c.bk * c.warps && wlds1_built(MT, c.warps, KS)) {
+  if (K == (int64_t)c.bk * c.warps && wlds1_built(MT, NC, c.warps, KS)) {
     switch (epi_kind(e)) {
       case EK_BF16: return launch_wlds1_w<MT, NC, KS, EK_BF16>(c.warps, a, lda, b, ldb, e, st);
       case EK_BF16_BBF16:
@@ -1269,11 +1327,15 @@ hipError_t launch_wlds_t(const i8l_config& c, const int8_t* a, int64_t lda, cons
       default: return launch_wlds1_w<MT, NC, KS, EK_ANY>(c.warps, a, lda, b, ldb, e, st);
     }
   }
-  switch (epi_kind(e)) {
-    case EK_BF16: return launch_wlds_k<MT, NC, KS, EK_BF16>(c, a, lda, b, ldb, e, K, st);
-    case EK_BF16_BBF16: return launch_wlds_k<MT, NC, KS, EK_BF16_BBF16>(c, a, lda, b, ldb, e, K, st);
-    default: return launch_wlds_k<MT, NC, KS, EK_ANY>(c, a, lda, b, ldb, e, K, st);
+  if constexpr (wlds_multi_fits(MT, NC, KS)) {
+    switch (epi_kind(e)) {
+      case EK_BF16: return launch_wlds_k<MT, NC, KS, EK_BF16>(c, a, lda, b, ldb, e, K, st);
+      case EK_BF16_BBF16:
+        return launch_wlds_k<MT, NC, KS, EK_BF16_BBF16>(c, a, lda, b, ldb, e, K, st);
+      default: return launch_wlds_k<MT, NC, KS, EK_ANY>(c, a, lda, b, ldb, e, K, st);
+    }
   }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
@@ -1287,6 +1349,8 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
   I8L_WLDS(2, 16, 2) I8L_WLDS(2, 16, 4) I8L_WLDS(2, 8, 2) I8L_WLDS(2, 8, 4)
   I8L_WLDS(4, 16, 2) I8L_WLDS(4, 16, 4) I8L_WLDS(4, 8, 2) I8L_WLDS(4, 8, 4)
   I8L_WLDS(8, 16, 2) I8L_WLDS(8, 8, 2)
+  I8L_WLDS(1, 32, 2) I8L_WLDS(1, 32, 4) I8L_WLDS(2, 32, 2) I8L_WLDS(2, 32, 4)
+  I8L_WLDS(4, 32, 2) I8L_WLDS(4, 32, 4)
 #undef I8L_WLDS
   return hipErrorInvalidValue;
 }
@@ -1447,10 +1511,25 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     }
   }
   // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
-  // direct-to-LDS ring; the activations are re-read N/128 times instead of N/16 or N/32.
-  if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 32 && N >= 6144))) {
+  // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
+  if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 64 && N >= 6144))) {
     *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
     return;
+  }
+  // 17 to 128 tokens: weights through LDS in 32-token x 32-column tiles (several row
+  // blocks above 32 tokens), 16 waves of one 128-byte step when K is 2048, else 4 waves
+  // stepping through their K slices.
+  if (M <= 128 && N % 32 == 0 && K % 128 == 0) {
+    const i8l_config one{32, 32, 128, 16, 3, 1, 1};
+    const i8l_config steps{32, 32, K % 1024 == 0 ? 256 : 128, 4, 3, 1, 1};
+    if (K == 2048 && N < 8192 && wlds_ok(one, K)) {
+      *c = one;
+      return;
+    }
+    if (wlds_ok(steps, K)) {
+      *c = steps;
+      return;
+    }
   }
   if (M <= 128) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
@@ -1591,9 +1670,9 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     err = hipGetLastError();
   } else if (c.stages == 1) {
     err = launch_stream(c, a, stride_am, b, stride_bn, e, (int)K, hs);
-  } else if (c.stages == 3 && c.bn <= 16) {
-    // the schedule keeps in-tile row offsets in 32 bits
-    if (stride_am > INT32_MAX / 32 || stride_bn > INT32_MAX / 16) {
+  } else if (c.stages == 3 && c.bn <= 32) {
+    // the schedule keeps in-tile row offsets (< 128 token rows, < 32 weight rows) in 32 bits
+    if (stride_am > INT32_MAX / 128 || stride_bn > INT32_MAX / 32) {
       const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
       hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
                          stride_bk, stride_bn, e, K);

@@ -63,6 +63,25 @@ def lib() -> ctypes.CDLL:
     return L
 
 
+FAST_NAME = "_i8l_fast"
+_fast_mod = None
+_fast_checked = False
+
+
+def fast():
+    """The C++ eager binding over this library (csrc/i8l_torch.cpp), or None when it is not
+    built, in which case every call goes through ctypes.  It launches the same kernels
+    through the same entry points; a binding that is built but does not import raises."""
+    global _fast_mod, _fast_checked
+    if not _fast_checked:
+        lib()
+        if any(LIB_PATH.parent.glob(FAST_NAME + ".*.so")):
+            import importlib
+            _fast_mod = importlib.import_module("int8_linear." + FAST_NAME)
+        _fast_checked = True
+    return _fast_mod
+
+
 def last_error() -> str:
     return lib().i8l_last_error().decode(errors="replace")
 

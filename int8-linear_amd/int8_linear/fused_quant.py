@@ -33,6 +33,18 @@ from int8_linear.kernel import NotSupported
 _ACT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
 
+def _fast(name: str, *args):
+    """The call through the C++ binding, or None (not built, or not the plain case: the
+    Python path below then handles it, with its own checks and errors)."""
+    f = _lib.fast()
+    if f is None:
+        return None
+    try:
+        return getattr(f, name)(*args)
+    except (TypeError, AttributeError):
+        return None
+
+
 def _act_code(t: torch.Tensor, what: str) -> int:
     code = _ACT.get(t.dtype)
     if code is None:
@@ -45,6 +57,9 @@ def _act_code(t: torch.Tensor, what: str) -> int:
 def add_rmsnorm_quant(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
                       eps: float, precise_div: bool = True):
     """(x_q int8 [M, K], scale fp32 [M, 1], residual_out [M, K] or None)."""
+    r = _fast("add_rmsnorm_quant", x, residual, weight, eps, precise_div)
+    if r is not None:
+        return r
     assert x.is_contiguous() and x.dim() == 2
     M, K = x.shape
     act = _act_code(x, "x")
@@ -71,6 +86,9 @@ def add_rmsnorm_quant(x: torch.Tensor, residual: torch.Tensor | None, weight: to
 
 def silu_mul_quant(gate_up: torch.Tensor, precise_div: bool = True, round_silu: bool = False):
     """silu(gate) * up, quantized: (x_q int8 [M, I], scale fp32 [M, 1])."""
+    r = _fast("silu_mul_quant", gate_up, precise_div, round_silu)
+    if r is not None:
+        return r
     assert gate_up.is_contiguous() and gate_up.dim() == 2
     M, I2 = gate_up.shape
     I = I2 // 2
@@ -93,6 +111,9 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
     x may be a column slice of a wider tensor (unit column stride, any row stride), such
     as the q columns of a qkv output: it is read in place, with no copy.
     """
+    r = _fast("quant_per_token", x, precise_div)
+    if r is not None:
+        return r
     assert x.dim() == 2 and (x.stride(1) == 1 or x.shape[1] <= 1)
     M, K = x.shape
     act = _act_code(x, "x")

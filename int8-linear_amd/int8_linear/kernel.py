@@ -123,6 +123,35 @@ def choose_config(m: int, n: int, k: int) -> Config:
     return cfg
 
 
+def _table_rows(device: int) -> list[list[int]]:
+    """This device's tuned table as rows (k, n, m, bm, bn, bk, warps, stages, group_m,
+    split_k), for the C++ binding's configuration lookup."""
+    rows = []
+    for kn, buckets in _device_table(device).items():
+        k, n = map(int, kn.split("x"))
+        for m, row in buckets.items():
+            c = Config(**row["config"])
+            rows.append([k, n, int(m), c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m,
+                         c.split_k])
+    return rows
+
+
+def _fast_mm(a_q, b_q, scale_a, scale_b, out_dtype, bias):
+    """The launch through the C++ binding, or None (not built, or not the plain case)."""
+    f = _lib.fast()
+    if f is None:
+        return None
+    try:
+        out = f.mm(a_q, b_q, scale_a, scale_b, out_dtype, bias)
+        if out is None and a_q.is_cuda and not f.has_table(a_q.get_device()):
+            # first call on this device: hand its tuned table over, then try again
+            f.set_table(a_q.get_device(), _table_rows(a_q.get_device()))
+            out = f.mm(a_q, b_q, scale_a, scale_b, out_dtype, bias)
+    except (TypeError, AttributeError):
+        return None  # not tensors or dtypes: the Python path reports it
+    return out
+
+
 def supported(m: int, n: int, k: int, config: Config | None = None) -> bool:
     """Whether w8a8_mm takes (M, N, K) under `config` (default: choose_config)."""
     cfg = config or default_config(m, n, k)
@@ -147,7 +176,15 @@ def w8a8_mm(
     a scalar, both float32.  With raw=True the exact int32 product is returned and the
     scales and bias are ignored.  cached_launch is accepted for API compatibility; every
     launch is a direct C call already.
+
+    Without an explicit config the call goes through the C++ binding when it is built,
+    which chooses the same configuration (by the operands' device) and launches the same
+    kernel; anything but the plain case comes back here.
     """
+    if config is None and not raw:
+        out = _fast_mm(a_q, b_q, scale_a, scale_b, out_dtype, bias)
+        if out is not None:
+            return out
     if a_q.dtype != torch.int8 or b_q.dtype != torch.int8:
         raise NotSupported(f"int8 operands only, got {a_q.dtype} and {b_q.dtype}")
     if a_q.dim() != 2 or b_q.dim() != 2 or a_q.shape[1] != b_q.shape[0]:

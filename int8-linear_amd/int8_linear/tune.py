@@ -52,7 +52,8 @@ DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
 WLDS_TILES = [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
               (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4),
-              (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2)]
+              (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2),
+              (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4)]
 
 
 def candidate_configs(m: int, k: int, n: int) -> list[Config]:
@@ -61,8 +62,8 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
     if m <= 128:
         need = next(mt for mt in (1, 2, 4, 8) if 16 * mt >= m)
         for mt, nc, ks in WLDS_TILES:
-            if mt not in (need, need // 2):
-                continue  # one row block covering M, or two half-size ones
+            if mt > need:
+                continue  # one row block covering M, or several smaller ones
             for w in (4, 8, 16):
                 cfg = Config(16 * mt, nc, 64 * ks, w, 3, 1)
                 if supported(m, n, k, cfg):
@@ -70,8 +71,8 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
     if m <= 256:
         need = next(mt for mt in (1, 2, 4, 8) if 16 * mt >= min(m, 128))
         for mt, bn in STREAM_TILES:
-            if mt not in (need, need // 2):
-                continue  # one row block covering M, or two half-size ones
+            if mt > need:
+                continue  # one row block covering M, or several smaller ones
             for w in (1, 2, 4, 8, 16):
                 cfg = Config(16 * mt, bn, 64 * w, w, 1, 1)
                 if supported(m, n, k, cfg):

@@ -34,13 +34,12 @@ _vllm_triton_scaled_mm = None
 def _run(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
          out_dtype: torch.dtype, bias: Optional[torch.Tensor]) -> torch.Tensor:
     global CALLS, FALLBACKS
-    m, k = a_q.shape
-    n = b_q.shape[1]
-    cfg = choose_config(m, n, k)
     CALLS += 1
-    CONFIGS.setdefault((m, k, n), cfg.name)
+    key = (a_q.shape[0], a_q.shape[1], b_q.shape[1])
+    if key not in CONFIGS:
+        CONFIGS[key] = choose_config(key[0], key[2], key[1]).name
     try:
-        return w8a8_mm(a_q, b_q, scale_a, scale_b, out_dtype, bias, config=cfg)
+        return w8a8_mm(a_q, b_q, scale_a, scale_b, out_dtype, bias)
     except NotSupported:
         if _vllm_triton_scaled_mm is None:
             raise

@@ -44,16 +44,18 @@ def test_default_config_regimes():
     assert d.stages == 3 and d.bm == 16 and 2048 % (d.bk * d.warps) == 0
     assert default_config(17, 4096, 2048).bm == 32          # one tile covers M=17
     assert default_config(1, 2048, 6144).bn == 8            # narrow N: 8 columns a workgroup
-    s = default_config(64, 4096, 2048)                      # register-streamed weights
+    s = default_config(64, 4096, 2048)                      # 32x32 tiles through LDS
+    assert (s.bm, s.bn, s.stages, s.warps) == (32, 32, 3, 16)
+    assert (default_config(128, 2048, 6144).bk, default_config(128, 2048, 6144).warps) == (256, 4)
+    s = default_config(64, 4104, 2056)                      # odd K: register-streamed weights
     assert s.stages == 1 and s.bm == 64 and s.bk == 64 * s.warps
-    assert default_config(128, 2048, 6144).bm == 128
     p = default_config(4096, 28672, 4096)
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
     assert default_config(300, 2048, 2048).stages >= 2
     mid = default_config(96, 12288, 2048)                   # 64-token overlapped-ring tiles
     assert (mid.bm, mid.bn, mid.stages) == (64, 128, 12)
     assert default_config(400, 2048, 6144).bm == 64
-    assert default_config(96, 4096, 2048).stages == 1       # narrower N keeps streaming
+    assert default_config(96, 4096, 2048).bn == 32          # narrower N: 32-column tiles
     for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
         assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
 
@@ -65,6 +67,9 @@ def test_supported_decline_rule_matches_reference():
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 3, 1))  # 64-byte steps: not built
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 256, 8, 3, 1))     # through LDS, 1 step
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 128, 4, 3, 1))     # 4 steps a wave
+    assert kernel.supported(16, 4096, 2048, Config(16, 32, 128, 16, 3, 1))    # 32 columns, 1 step
+    assert kernel.supported(16, 4096, 2048, Config(16, 32, 128, 8, 3, 1))     # ... or 2 steps
+    assert not kernel.supported(16, 4096, 2048, Config(16, 64, 128, 8, 3, 1))  # 64: not built
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 384, 4, 3, 1))  # K % (bk*warps)
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 512, 16, 3, 1))  # LDS > 160 KiB
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
@@ -136,3 +141,38 @@ def test_cpu_tensors_are_declined_not_computed():
     a = torch.zeros((2, 64), dtype=torch.int8)
     with pytest.raises(NotSupported):
         kernel.w8a8_mm(a, torch.zeros((64, 16), dtype=torch.int8), torch.ones(1), torch.ones(1))
+
+
+def test_cpp_binding_loads_and_chooses_the_tuned_config():
+    """The C++ eager binding chooses the configuration kernel.tuned_config / default_config
+    would: the largest tuned bucket at or below M, else the library's default."""
+    from int8_linear import kernel as kn
+    f = _lib.fast()
+    assert f is not None, "the binding is built with the library"
+    for name in ("mm", "add_rmsnorm_quant", "silu_mul_quant", "quant_per_token", "set_table"):
+        assert hasattr(f, name)
+    rows = [[2048, 4096, 1, 16, 16, 512, 8, 1, 1, 1], [2048, 4096, 17, 32, 16, 512, 8, 1, 1, 1]]
+    f.set_table(7, rows)
+    assert f.has_table(7) and not f.has_table(6)
+    assert f.config_for(6, 1, 4096, 2048) is None
+    assert f.config_for(7, 1, 4096, 2048)[:2] == (16, 16)
+    assert f.config_for(7, 16, 4096, 2048)[:2] == (16, 16)
+    assert f.config_for(7, 17, 4096, 2048)[:2] == (32, 16)
+    assert f.config_for(7, 500, 4096, 2048)[:2] == (32, 16)
+    for m, n, k in ((5, 2048, 2048), (4096, 4096, 4096), (96, 12288, 2048)):
+        d = kn.default_config(m, n, k)
+        assert f.config_for(7, m, n, k) == (d.bm, d.bn, d.bk, d.warps, d.stages, d.group_m,
+                                            d.split_k)
+
+
+def test_cpp_binding_declines_what_the_python_path_must_handle():
+    import torch
+    f = _lib.fast()
+    a = torch.zeros((2, 64), dtype=torch.int8)
+    assert f.mm(a, torch.zeros((64, 16), dtype=torch.int8), torch.ones(1), torch.ones(1),
+                torch.bfloat16, None) is None                        # host tensors
+    x = torch.zeros((2, 64), dtype=torch.bfloat16)
+    assert f.add_rmsnorm_quant(x, None, torch.ones(64, dtype=torch.bfloat16), 1e-6, True) is None
+    assert f.silu_mul_quant(x, True, False) is None
+    assert f.quant_per_token(x, True) is None
+    assert f.launches() == 0

@@ -92,12 +92,14 @@ def test_exact_under_other_tilings(config, m):
     assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
 
 
-# The weights-through-LDS decode schedule (stages 3, bm <= 32): every built tile, with one,
-# two, three and four K steps a wave (the ring's even and odd tails), 16/8/4 columns a
+# The weights-through-LDS decode schedule (stages 3, bm <= 128): every built tile, with one,
+# two, three and four K steps a wave (the ring's even and odd tails), 32/16/8/4 columns a
 # workgroup, ragged M.
 WLDS = [(mt, nc, ks) for mt, nc, ks in
         [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
-         (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4)]]
+         (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4),
+         (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2),
+         (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4)]]
 
 
 @pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
