@@ -18,7 +18,8 @@ bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3
 oracle's CPU restatement of the reference's path, on a bounded sample).
 
     python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
-    python bench.py --only standin       # one extra section alone (quant|prefill|standin|launch)
+    python bench.py --only standin       # one extra section alone
+                                         # (quant|prefill|standin|launch|llama_decode)
 Every GPU output is checked against a float64 reference before it is timed, after the
 output buffer has been poisoned.  Prints ONE JSON line.
 """
@@ -228,7 +229,8 @@ def main() -> int:
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
-    ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch"], default=None,
+    ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch", "llama_decode"],
+                    default=None,
                     help="run one extra section alone (for profiling) and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -250,7 +252,7 @@ def main() -> int:
         return 0
     if args.only:
         fn = {"quant": bench_quant, "prefill": bench_prefill, "standin": bench_standin,
-              "launch": bench_launch}[args.only]
+              "launch": bench_launch, "llama_decode": bench_llama_decode}[args.only]
         print(json.dumps({args.only: fn(dev)}), flush=True)
         return 0
     shapes = SHAPES["qwen3-1.7b-vllm"]
@@ -325,6 +327,7 @@ def main() -> int:
             table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
         result["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
         result["quant"] = bench_quant(dev)
+        result["llama_decode"] = bench_llama_decode(dev)
         result["prefill"] = bench_prefill(dev)
         result["standin"] = bench_standin(dev)
         result["launch"] = bench_launch(dev)
@@ -379,6 +382,42 @@ def bench_standin(dev) -> dict:
             "layers": standin.LAYERS, "weight_bytes_per_layer": int(wbytes),
             "step": "add_rmsnorm_quant > qkv > quant(q cols) > o > add_rmsnorm_quant > gate_up "
                     "> silu_mul_quant > down, one HIP graph per 28-layer step"}
+
+
+LLAMA_DECODE_M = [1, 4, 16]
+
+
+def bench_llama_decode(dev) -> dict:
+    """Decode on the Llama-3-8B shapes (the larger of the two models BASELINE names for the
+    HBM target at M <= 16): µs per linear and fraction of 8 TB/s, weights rotating through
+    >= 768 MiB of copies so every call reads them from HBM."""
+    import torch
+
+    from int8_linear import w8a8_mm
+    from int8_linear.operands import operands, seed_of
+    from int8_linear.shapes import SHAPES
+    rows = []
+    for label, k, n in SHAPES["llama-3-8b"]:
+        d = operands(16, k, n, seed_of(16, k, n), device=dev)
+        copies = max(2, -(-ROTATE_BYTES // (k * n)))
+        ws = [d["w_q"]] + [d["w_q"].clone() for _ in range(copies - 1)]
+        w_s = d["w_s"]
+        for m in LLAMA_DECODE_M:
+            a = operands(m, k, 64, seed_of(m, k, n), device=dev)
+            a_q, a_s = a["a_q"], a["a_s"]
+            out = w8a8_mm(a_q, ws[0].t(), a_s, w_s, torch.bfloat16)
+            term = (a_q.double() @ ws[0].double().t()) * a_s.double() * w_s.double().t()
+            err = ((out.double() - term).abs() / term.abs().clamp_min(1e-6)).max().item()
+            if not err <= 1e-2:
+                raise SystemExit(f"FAIL llama decode {label} M={m}: rel err {err}")
+            us = graph_time_us(lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s,
+                                                 torch.bfloat16), 2 * copies, 3)
+            frac = gemm_bytes(m, k, n, False) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS
+            rows.append([label, m, round(us, 2), round(frac, 3)])
+            log(f"llama decode {label} M={m}: {us:.2f} us, {frac:.1%} of HBM")
+        del ws, d
+        torch.cuda.empty_cache()
+    return {"cols": ["shape", "M", "us", "hbm_frac"], "rows": rows}
 
 
 LAUNCH_SHAPES = [("q_proj, o_proj", 2048, 2048), ("gate_up_proj", 2048, 12288)]

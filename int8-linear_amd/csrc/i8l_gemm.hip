@@ -1513,7 +1513,11 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
   // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
   if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 64 && N >= 6144))) {
-    *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
+    // very wide N has tiles enough for 128-token rows, which halve the weights' re-reads
+    if (N >= 16384)
+      *c = i8l_config{128, 128, 128, 4, 4 + kPipelined, 8, 1};
+    else
+      *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
     return;
   }
   // 17 to 128 tokens: weights through LDS in 32-token x 32-column tiles (several row
