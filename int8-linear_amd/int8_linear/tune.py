@@ -5,6 +5,11 @@ reference's sweep and merge are bench/bench_linear.py:213-227, 385-389).
 
     python -m int8_linear.tune --shapes qwen3-1.7b-vllm --m 1,2,4,8,16,17,32,64,128
     python -m int8_linear.tune --shapes llama-3-8b --m 512,1024,2048,4096 --merge
+    python -m int8_linear.tune --shapes qwen3-1.7b-vllm --m capture --merge
+
+`--m capture` is vLLM's CUDA-graph batch sizes (1, 2, 4, 8 to 248 by 8, 256 to 512 by 16)
+plus three prefill sizes, the M values a served decode step is padded to (the reference's
+tools/run_e2e_vm.sh:60-67).
 
 Timing is graph replay of back-to-back calls whose weights rotate through >= 512 MiB of
 copies, so each call reads its weights from HBM rather than from the 256 MiB Infinity
@@ -54,6 +59,14 @@ WLDS_TILES = [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 
               (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4),
               (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2),
               (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4)]
+
+
+CAPTURE_SIZES = [1, 2, 4, *range(8, 256, 8), *range(256, 513, 16), 1024, 2048, 4096]
+
+
+def parse_ms(spec: str) -> list[int]:
+    """A comma-separated list of M values, or `capture` for vLLM's graph batch sizes."""
+    return list(CAPTURE_SIZES) if spec == "capture" else [int(x) for x in spec.split(",")]
 
 
 def candidate_configs(m: int, k: int, n: int) -> list[Config]:
@@ -171,13 +184,14 @@ def main() -> int:
     from int8_linear.shapes import SHAPES
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default="qwen3-1.7b-vllm")
-    ap.add_argument("--m", default="1,2,4,8,16,17,32,64,128")
+    ap.add_argument("--m", default="1,2,4,8,16,17,32,64,128",
+                    help="comma-separated M values, or capture (vLLM graph batch sizes)")
     ap.add_argument("--merge", action="store_true", help="write the result into tuned_configs.json")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
     dev = torch.device("cuda:0")
     arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
-    ms = [int(x) for x in args.m.split(",")]
+    ms = parse_ms(args.m)
     table = {}
     for label, k, n in SHAPES[args.shapes]:
         table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True))
