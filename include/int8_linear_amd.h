@@ -46,9 +46,12 @@ enum {
  * (reference int8_linear/kernel.py:49-60) with the MI355X meaning of each field:
  *   bm, bn, bk : output rows (tokens) x output columns x K bytes per workgroup step
  *   warps      : wavefronts (64 lanes) per workgroup
- *   stages     : LDS buffers for the staged (prefill) schedule, 1 or 2
+ *   stages     : the schedule: 1 weights streamed into registers (decode); 3 with bm <= 128
+ *                and bn <= 32 weights through LDS (decode); 2 LDS staged through registers,
+ *                3..8 a ring of that many direct-to-LDS buffers, >= 11 the same ring of
+ *                stages - 8 buffers with fragment reads overlapped with the MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order)
- *   split_k    : K-splits inside one workgroup (decode schedule), each wave sums one slice
+ *   split_k    : reserved; must be 1
  * A config the library was not built for returns I8L_UNSUPPORTED.
  */
 typedef struct i8l_config {
@@ -134,6 +137,33 @@ int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale,
 int i8l_quant_per_token(const void* x, int64_t ldx, int8_t* q, float* scale,
                         int64_t M, int64_t H, int32_t act_dtype,
                         int32_t precise_div, void* stream);
+
+/*
+ * The per-token quantizer and the W8A8 matmul in one launch, for few tokens:
+ *   out = i8l_w8a8_mm(quant(x), b, scale_a = the quantizer's scales, scale_b, bias)
+ * bit for bit, where quant is i8l_quant_per_token.  x is bf16/f16 [M,K] with row stride ldx
+ * (a multiple of 8 elements, >= K; a column slice such as the q columns of a qkv output is
+ * read in place) and a 16-byte aligned base.  Every column tile quantizes its token rows
+ * itself, so the work grows with M times the number of column tiles: the host layer takes
+ * this path for M <= 8 (the library takes any M and gives the same bits).  scale_a_out, if not NULL, receives the M per-token scales.
+ * b must be K-contiguous (stride_bk == 1) and 16-byte aligned, out 16-byte aligned with
+ * 16-byte row pitch; anything else returns I8L_UNSUPPORTED (use the two calls).  cfg is a
+ * single-step weights-through-LDS tile with 16 waves (bm 16, bn 8/16/32, bk 128 or 256,
+ * stages 3, K == 16 * bk) or NULL for the library's choice.
+ *
+ * Replaces the pair the reference's stand-in issues per o_proj, vLLM's scaled_int8_quant
+ * then _w8a8_mm (bench/fuse_quant.py:233-235 of AshrithaG/int8-linear; kernel.py:202-257).
+ */
+int i8l_w8a8_mm_dynq(const void* x, int64_t ldx, int32_t act_dtype, int32_t precise_div,
+                     const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                     const float* scale_b, int64_t scale_b_len,
+                     const void* bias, int32_t bias_dtype,
+                     void* out, int64_t stride_cm, int32_t out_dtype, float* scale_a_out,
+                     int64_t M, int64_t N, int64_t K,
+                     const i8l_config* cfg, void* stream);
+
+/* Whether i8l_w8a8_mm_dynq takes (M,N,K,cfg) (cfg NULL: the library's choice); host-only. */
+int i8l_w8a8_mm_dynq_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
 
 /* Thread-local description of the last failure ("" if none). */
 const char* i8l_last_error(void);

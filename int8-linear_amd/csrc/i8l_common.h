@@ -117,6 +117,33 @@ __device__ __forceinline__ float canon_rsqrtf(float v) {
   return (float)(1.0 / __builtin_sqrt((double)v));
 }
 
+// ---------------------------------------------------------------- cross-lane moves
+// DPP controls (gfx9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
+constexpr int kQuadSwap1 = 0xB1, kQuadSwap2 = 0x4E, kHalfMirror = 0x141, kRowMirror = 0x140;
+// ds_swizzle bitmask mode: lane ^ 16 within each 32-lane half.
+constexpr int kSwizzleXor16 = 0x401F;
+
+// Every control used is a full permutation, so no lane reads an invalid source.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+// Maximum over each aligned group of G lanes (G = 16, 32 or 64); every lane returns its
+// group's.  Four DPP steps cover a 16-lane row; a swizzle and a permute cover 32 and 64.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
+  v = fmaxf(v, __int_as_float(dpp_i<kQuadSwap1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<kQuadSwap2>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<kHalfMirror>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_i<kRowMirror>(__float_as_int(v))));
+  if constexpr (G >= 32)
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwizzleXor16)));
+  if constexpr (G == 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
 // ---------------------------------------------------------------- errors
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* where);

@@ -702,6 +702,172 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
   }
 }
 
+// ------------------------------------------------------------------ dynamic-quant decode
+// gemm_wlds1 with the per-token activation quantizer folded in, for one 16-token row block.
+// A arrives as the bf16/fp16 X [M, K] that quant_per_token would quantize; each wave
+// quantizes its own K slice of the block's valid rows, with each row's absmax combined
+// across the lanes holding it and then across the waves.  The arithmetic is the quantizer
+// kernel's (absmax of |x|, scale = absmax/127, codes = rint(x * 127/absmax) clamped to
+// [-128, 127]; reference fused_quant.py:41-53), so the output equals quant_per_token followed
+// by w8a8_mm bit for bit, from one kernel instead of two.
+//
+// Every column tile repeats the row work, so the layout keeps it proportional to the valid
+// rows: a wave reads its slice as 16-byte chunks of 8 values, CH = S/8 chunks a row and
+// 64/CH rows a pass over the lanes, quantizes them, and writes the codes to an LDS tile of
+// 16 rows x S bytes, from which the MFMA fragments are read (rows past M read as zero).
+template <int NC, int KS, int W, int P, int EK, int DT>
+__global__ void __launch_bounds__(64 * W)
+gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ B,
+              int64_t ldb, Epi e, float* __restrict__ sa_out, int precise) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;
+  constexpr int NI = SB / 1024;
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int NCF = NC < 16 ? NC : 16;
+  constexpr int NF = NC / NCF;
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  static_assert(NF <= W, "every fragment needs a storing wave");
+  constexpr int CH = S / 8;                  // 8-value chunks of a row in a wave's slice
+  constexpr int RPP = 64 / CH;               // rows a pass covers
+  static_assert(RPP * CH == 64 && 16 % RPP == 0, "rows must split over the lanes");
+  static_assert(P >= 1 && P * RPP <= 16, "P passes of RPP rows cover the block's valid rows");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * 16;
+  // valid rows of the block; the host picks P = ceil(mb / RPP), so every pass is needed and
+  // the code has no skipped (taken-branch) passes
+  const int mb = (int)min((int64_t)16, (int64_t)e.M - m0);
+  const int64_t kw = (int64_t)wave * S;
+  int8_t* wbuf = lds + (size_t)wave * SB;
+  v4i* red = (v4i*)(lds + (size_t)W * SB);                          // [W][NF][64]
+  float* rmax = (float*)(lds + (size_t)W * SB + (size_t)W * NF * 1024);  // [W][16]
+  float* scl = rmax + W * 16;               // [W][16]: each wave's copy of the row scales
+  int8_t* abuf = lds + (size_t)W * SB + (size_t)W * NF * 1024 + (size_t)W * 128 + wave * 16 * S;
+
+  // The activations are requested first and waited for alone: the quantizer work below
+  // then runs while the weights' DMA is still in flight.
+  // pass p: lane l holds chunk l % CH of row p*RPP + l/CH (rows past M are not read)
+  const int crow = lane / CH, cchunk = lane % CH;
+  uint4 xr[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    xr[p] = uint4{0, 0, 0, 0};
+    const int r = p * RPP + crow;
+    if (r < mb) xr[p] = *(const uint4*)(X + (m0 + r) * ldx + kw + 8 * cchunk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  lds_i8_t* dst = (lds_i8_t*)wbuf;
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                     16, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt_wlds<NI>();  // vector loads complete in issue order: the activations are in
+
+  auto elem = [&](const uint4& v, int k) -> float {
+    const uint32_t w32 = k < 4 ? (k < 2 ? v.x : v.y) : (k < 6 ? v.z : v.w);
+    return act_to_f32<DT>((k & 1) ? (w32 >> 16) : (w32 & 0xffffu));
+  };
+  // absmax of each valid row's slice: a lane's chunk, then the CH lanes of the row
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(elem(xr[p], k)));
+    am = group_max<CH>(am);
+    if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
+  }
+  __syncthreads();
+  auto row_scale = [&](int r, float& scale, float& inv) {
+    float absmax = rmax[r];
+#pragma unroll
+    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + r]);
+    const float s_div = absmax / 127.0f;
+    const float i_div = absmax == 0.0f ? 0.0f : 127.0f / absmax;
+    const float s_rcp = absmax * (1.0f / 127.0f);
+    const float i_rcp = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
+    scale = precise ? s_div : s_rcp;
+    inv = precise ? i_div : i_rcp;
+  };
+  // codes of each valid chunk into the wave's LDS tile (row pitch S bytes)
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = p * RPP + crow;
+    if (r < mb) {
+      float scale, inv;
+      row_scale(r, scale, inv);
+      uint32_t word[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float v = __builtin_rintf(elem(xr[p], 4 * q + b) * inv);
+          v = fminf(fmaxf(v, -128.0f), 127.0f);
+          packed |= ((uint32_t)(int)v & 0xffu) << (8 * b);
+        }
+        word[q] = packed;
+      }
+      *(uint2*)(abuf + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
+      if (cchunk == 0) {
+        scl[wave * 16 + r] = scale;
+        if (sa_out != nullptr && blockIdx.x == 0 && wave == 0) sa_out[m0 + r] = scale;
+      }
+    }
+  }
+  Cols4 cl;
+  const int64_t mrow = m0 + r16;
+  const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+  if (wave < NF) cl = load_cols4<EK>(e, ncol);
+  wait_vmcnt_wlds<0>();  // the weights, and the epilogue operands
+  // the wave's own LDS writes are complete before its reads below (LDS is in order per wave)
+  v4i a[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    a[s] = r16 < mb ? *(const v4i*)(abuf + r16 * S + 64 * s + 16 * grp) : v4i{0, 0, 0, 0};
+
+  v4i b[KS][NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      b[s][f] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+  }
+  v4i acc[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) acc[f] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s], acc[f], 0, 0, 0);
+
+#pragma unroll
+  for (int f = 0; f < NF; ++f) red[(wave * NF + f) * 64 + lane] = acc[f];
+  __syncthreads();
+  if (wave < NF) {
+    v4i sum = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[(w * NF + wave) * 64 + lane];
+    // this wave's own scale of row r16 (written above by this wave: LDS is in order)
+    if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, scl[wave * 16 + r16]);
+  }
+}
+
 // ------------------------------------------------------------------ staged schedule
 // Workgroup = WM x WN waves over a BM (tokens) x BN (columns) tile; K advances BK bytes per
 // step through two LDS buffers.  Each LDS tile row (one token or one weight row) holds BK
@@ -1481,6 +1647,110 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int elt_size(int dt) { return dt == I8L_BF16 || dt == I8L_F16 ? 2 : 4; }
 
+// Dynamic-quant decode tiles (gemm_wlds1_dq, one 16-token row block): (NC, KS, W) with
+// K == 64 * KS * W.  The config's bm is 16 and its stages 3, as for gemm_wlds1.
+struct DqTile {
+  int nc, ks, w;
+};
+constexpr DqTile kDq[] = {{8, 2, 16}, {16, 2, 16}, {32, 2, 16}, {8, 4, 16}, {16, 4, 16}};
+
+size_t dq_lds_bytes(int nc, int ks, int W) {
+  const int nf = nc > 16 ? nc / 16 : 1;
+  // weights, the cross-wave sums, the row maxima and scales, the 16-row code tiles
+  return (size_t)W * nc * 64 * ks + (size_t)W * nf * 1024 + (size_t)W * 128 +
+         (size_t)W * 16 * 64 * ks;
+}
+
+bool dq_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 3 || c.split_k != 1 || c.bm != 16) return false;
+  for (auto t : kDq)
+    if (t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
+      return K == (int64_t)64 * t.ks * t.w && dq_lds_bytes(t.nc, t.ks, t.w) <= kMaxLds;
+  return false;
+}
+
+// The untuned choice: 16 waves that take K in one step each, 16 columns a workgroup (8 for
+// narrow N).
+bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
+  const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : 8;
+  for (int ks : {2, 4}) {
+    const i8l_config t{16, nc, 64 * ks, 16, 3, 1, 1};
+    if (K == (int64_t)64 * ks * 16 && dq_ok(t, K)) {
+      *c = t;
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int NC, int KS, int W, int P, int EK, int DT>
+hipError_t launch_dq_k(const uint16_t* x, int64_t ldx, const int8_t* b, int64_t ldb,
+                       const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  auto kern = gemm_wlds1_dq<NC, KS, W, P, EK, DT>;
+  const size_t shm = dq_lds_bytes(NC, KS, W);
+  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
+  if (!attr_set && shm > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)shm);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  const dim3 grid(e.N / NC, (e.M + 15) / 16);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, x, ldx, b, ldb, e, sa_out, precise);
+  return hipGetLastError();
+}
+
+template <int NC, int KS, int W, int P>
+hipError_t launch_dq_p(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  if (act_dtype == I8L_F16)
+    return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_F16>(x, ldx, b, ldb, e, sa_out, precise, st);
+  switch (epi_kind(e)) {
+    case EK_BF16:
+      return launch_dq_k<NC, KS, W, P, EK_BF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
+                                                          st);
+    case EK_BF16_BBF16:
+      return launch_dq_k<NC, KS, W, P, EK_BF16_BBF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out,
+                                                                precise, st);
+    default:
+      return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
+                                                         st);
+  }
+}
+
+// Passes of the quantizer prologue: ceil(rows / RPP) for the block's valid rows, taken as
+// the next power of two (P in {1, 2, 4, ...}, at most 16 rows).
+template <int NC, int KS, int W>
+hipError_t launch_dq_t(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  constexpr int RPP = 64 / (8 * KS);
+  const int rows = e.M < 16 ? e.M : 16;
+  const int need = (rows + RPP - 1) / RPP;
+  if (need <= 1)
+    return launch_dq_p<NC, KS, W, 1>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if (need <= 2)
+    return launch_dq_p<NC, KS, W, 2>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if constexpr (16 / RPP >= 4)
+    if (need <= 4)
+      return launch_dq_p<NC, KS, W, 4>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if constexpr (16 / RPP >= 8)
+    if (need <= 8)
+      return launch_dq_p<NC, KS, W, 8>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
+                     const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
+                     hipStream_t st) {
+  const int nc = c.bn, ks = c.bk / 64, W = c.warps;
+#define I8L_DQ(NC_, KS_, W_)                                                                \
+  if (nc == NC_ && ks == KS_ && W == W_)                                                    \
+    return launch_dq_t<NC_, KS_, W_>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  I8L_DQ(8, 2, 16) I8L_DQ(16, 2, 16) I8L_DQ(32, 2, 16) I8L_DQ(8, 4, 16) I8L_DQ(16, 4, 16)
+#undef I8L_DQ
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
 
 void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
@@ -1692,4 +1962,97 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     err = launch_dma(dma_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   }
   return hip_status(err, "i8l_w8a8_mm launch");
+}
+
+extern "C" int i8l_w8a8_mm_dynq_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg) {
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_dq_config(N, K, &c)) {
+    set_error("no built dynamic-quant tile takes K=%lld in one step a wave", (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  if (M < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+    set_error("sizes out of range");
+    return I8L_UNSUPPORTED;
+  }
+  if (c.bn <= 0 || N % c.bn || !dq_ok(c, K)) {
+    set_error("config %dx%dx%d w%d s%d is not a built dynamic-quant tile for N=%lld K=%lld",
+              c.bm, c.bn, c.bk, c.warps, c.stages, (long long)N, (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  return I8L_OK;
+}
+
+extern "C" int i8l_w8a8_mm_dynq(const void* x, int64_t ldx, int32_t act_dtype,
+                                int32_t precise_div, const int8_t* b, int64_t stride_bk,
+                                int64_t stride_bn, const float* scale_b, int64_t scale_b_len,
+                                const void* bias, int32_t bias_dtype, void* out,
+                                int64_t stride_cm, int32_t out_dtype, float* scale_a_out,
+                                int64_t M, int64_t N, int64_t K, const i8l_config* cfg,
+                                void* stream) {
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("negative size M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    return I8L_INVALID_ARG;
+  }
+  if (act_dtype != I8L_BF16 && act_dtype != I8L_F16) {
+    set_error("activations must be bf16 or fp16 (code %d)", act_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (out_dtype != I8L_BF16 && out_dtype != I8L_F16 && out_dtype != I8L_F32) {
+    set_error("unsupported output dtype code %d", out_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (scale_b_len != 1 && scale_b_len != N) {
+    set_error("scale_b has %lld values for N=%lld", (long long)scale_b_len, (long long)N);
+    return I8L_INVALID_ARG;
+  }
+  if (bias_dtype != I8L_DTYPE_NONE && bias_dtype != I8L_BF16 && bias_dtype != I8L_F16 &&
+      bias_dtype != I8L_F32) {
+    set_error("unsupported bias dtype code %d", bias_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if ((bias_dtype == I8L_DTYPE_NONE) != (bias == nullptr)) {
+    set_error("bias pointer and bias dtype disagree");
+    return I8L_INVALID_ARG;
+  }
+  if (ldx < K) {
+    set_error("row stride %lld of x is below K=%lld", (long long)ldx, (long long)K);
+    return I8L_INVALID_ARG;
+  }
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_dq_config(N, K, &c)) {
+    set_error("no built dynamic-quant tile takes K=%lld in one step a wave", (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  const int st = i8l_w8a8_mm_dynq_supported(M, N, K, &c);
+  if (st != I8L_OK) return st;
+  if (M == 0 || N == 0) return I8L_OK;
+  const int osz = elt_size(out_dtype);
+  const bool layout = stride_bk == 1 && aligned16(b) && stride_bn % 16 == 0 &&
+                      stride_bn <= INT32_MAX / 32 && aligned16(x) && ldx % 8 == 0 &&
+                      aligned16(out) && (stride_cm * osz) % 16 == 0 && stride_cm >= N &&
+                      N % 4 == 0 && (scale_b_len == 1 || aligned16(scale_b)) &&
+                      (bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
+  if (!layout) {
+    set_error("the dynamic-quant path needs K-contiguous 16-byte aligned operands");
+    return I8L_UNSUPPORTED;
+  }
+  Epi e;
+  e.sa = nullptr;
+  e.sb = scale_b;
+  e.bias = bias;
+  e.out = out;
+  e.ldc = stride_cm;
+  e.sa_per_row = 1;
+  e.sb_per_col = scale_b_len == N && N > 1;
+  e.bias_dtype = bias_dtype;
+  e.out_dtype = out_dtype;
+  e.M = (int)M;
+  e.N = (int)N;
+  const hipError_t err = launch_dq(c, act_dtype, (const uint16_t*)x, ldx, b, stride_bn, e,
+                                   scale_a_out, precise_div ? 1 : 0, (hipStream_t)stream);
+  return hip_status(err, "i8l_w8a8_mm_dynq launch");
 }

@@ -35,16 +35,7 @@ namespace {
 constexpr int kMaxWaves = 16;  // waves per workgroup (1024 threads)
 
 // ------------------------------------------------------------------ cross-lane moves
-// DPP controls (gfx9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror.
-constexpr int kQuadSwap1 = 0xB1, kQuadSwap2 = 0x4E, kHalfMirror = 0x141, kRowMirror = 0x140;
-// ds_swizzle bitmask mode: lane ^ 16 within each 32-lane half.
-constexpr int kSwizzleXor16 = 0x401F;
-
-// Every control used is a full permutation, so no lane reads an invalid source.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
-}
+// (DPP controls and dpp_i are in i8l_common.h)
 template <int CTRL>
 __device__ __forceinline__ double dpp_d(double v) {
   const uint64_t u = __builtin_bit_cast(uint64_t, v);

@@ -7,6 +7,7 @@ that quantizer into the op that produces the input, one workgroup per token row:
     rmsnorm_quant(x, w, eps)               -> (x_q, scale)
     silu_mul_quant(gate_up)                -> (x_q, scale)
     quant_per_token(x)                     -> (x_q, scale)
+    quant_mm(x, b_q, scale_b)              -> w8a8_mm(*quant_per_token(x), b_q, ...)
 
 Same Python surface and arithmetic as the reference's int8_linear/fused_quant.py
 (AshrithaG/int8-linear, 41-124): residual add and norm in fp32, the normalized value rounded
@@ -125,6 +126,77 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
                                                 K, act, int(bool(precise_div)), _lib.stream_of(x))
         _lib.check(status, NotSupported)
     return q, s
+
+
+# Largest M that quant_mm takes.  Every column tile quantizes the token rows itself, so the
+# fused launch pays off only for few tokens: measured on MI355X at K = N = 2048 (graph replay,
+# cold weights), one launch vs quant_per_token + w8a8_mm is 4.45 vs 5.31 us at M = 1,
+# 5.19 vs 5.93 at M = 8 and 7.07 vs 6.30 at M = 16.
+QUANT_MM_MAX_M = 8
+
+
+def quant_mm(x: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
+             out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None,
+             precise_div: bool = True, *, config=None, return_scale: bool = False):
+    """quant_per_token(x) followed by w8a8_mm, as one kernel, for up to QUANT_MM_MAX_M tokens.
+
+    Bit for bit w8a8_mm(*quant_per_token(x, precise_div), b_q, ..., scale_b, out_dtype,
+    bias): the same quantizer arithmetic runs inside the GEMM (reference fused_quant.py:41-53
+    and kernel.py:202-257 in one launch).  x is bf16/fp16 [M, K], contiguous or a column
+    slice with unit column stride; b_q the K-contiguous [K, N] view of an [N, K] weight.
+    Raises NotSupported for more tokens, for a K that no single-step tile takes, or for
+    layouts the fused kernel does not read (the caller then makes the two calls).
+    """
+    from int8_linear.kernel import Config, _cconfig
+    if x.dim() != 2 or b_q.dim() != 2 or x.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(x.shape)} by {tuple(b_q.shape)}")
+    act = _act_code(x, "x")
+    if b_q.dtype != torch.int8 or not b_q.is_cuda:
+        raise NotSupported("b_q must be an int8 HIP tensor")
+    M, K = x.shape
+    N = b_q.shape[1]
+    if M > QUANT_MM_MAX_M:
+        raise NotSupported(f"quant_mm takes up to {QUANT_MM_MAX_M} tokens, got {M}")
+    if x.stride(1) != 1 and K > 1:
+        raise NotSupported("x needs a unit column stride")
+    sb = scale_b.reshape(-1).contiguous()
+    if sb.dtype != torch.float32:
+        raise NotSupported(f"float32 scale_b only, got {sb.dtype}")
+    if sb.numel() not in (1, N):
+        raise ValueError(f"scale_b has {sb.numel()} values for N={N}")
+    if bias is not None:
+        if tuple(bias.shape) != (N,):
+            raise ValueError(f"bias must have shape ({N},), got {tuple(bias.shape)}")
+        bias = bias.contiguous()
+        bias_code = _lib.DTYPE_CODE.get(bias.dtype)
+        if bias_code not in (_lib.BF16, _lib.F16, _lib.F32):
+            raise NotSupported(f"bias dtype {bias.dtype} is not supported")
+    else:
+        bias_code = _lib.DTYPE_NONE
+    out_code = _lib.DTYPE_CODE.get(out_dtype)
+    if out_code not in (_lib.BF16, _lib.F16, _lib.F32):
+        raise NotSupported(f"output dtype {out_dtype} is not supported")
+    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device) if return_scale else None
+    ldx = x.stride(0) if M > 1 else K
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    status = _lib.lib().i8l_w8a8_mm_dynq(
+        x.data_ptr(), ldx, act, int(bool(precise_div)), b_q.data_ptr(), b_q.stride(0),
+        b_q.stride(1), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
+        out.stride(0), out_code, s.data_ptr() if s is not None else None, M, N, K, cfg,
+        _lib.stream_of(x))
+    _lib.check(status, NotSupported)
+    return (out, s) if return_scale else out
+
+
+def quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
+    """Whether quant_mm takes (M, N, K) (under `config`, default the library's choice)."""
+    from int8_linear.kernel import Config, _cconfig
+    if m > QUANT_MM_MAX_M:
+        return False
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    return _lib.lib().i8l_w8a8_mm_dynq_supported(m, n, k, cfg) == _lib.OK
 
 
 # Numerics the custom ops use (reference fused_quant.py:127-129 defaults);

@@ -14,7 +14,9 @@ The first layer normalizes without a residual, as `rmsnorm_quant` does.
 
 The reference slices the q columns with .contiguous() and then quantizes them
 (bench/fuse_quant.py:233-234). Here the per-token quantizer reads the slice in place, so
-each layer issues 8 kernels instead of 9, and the values are the same.
+each layer issues 8 kernels instead of 9, and the values are the same.  Up to
+fused_quant.QUANT_MM_MAX_M tokens, the quantizer and o_proj are one kernel
+(fused_quant.quant_mm), which again gives the same bits: 7 kernels a layer.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
@@ -73,6 +75,11 @@ class DecoderStandIn:
         other.x = torch.randn((m, HIDDEN), generator=g).to(torch.bfloat16).to(self.x.device)
         return other
 
+    @property
+    def fused_o(self) -> bool:
+        """Whether o_proj takes its input unquantized (quantizer folded into the GEMM)."""
+        return fq.quant_mm_supported(self.m, HIDDEN, Q_COLS)
+
     def weight_bytes(self) -> int:
         return sum(w.numel() + 4 * s.numel() for layer in self.layers for w, s in layer.values())
 
@@ -82,6 +89,7 @@ class DecoderStandIn:
 
     def forward(self) -> torch.Tensor:
         """One step through every layer; returns the last down_proj output [m, HIDDEN]."""
+        fused_o = self.fused_o
         res = self.x
         q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
         h = None
@@ -89,8 +97,12 @@ class DecoderStandIn:
             if i:
                 q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
             a = self.mm(layer, "qkv_proj", q, s)
-            q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
-            h = self.mm(layer, "o_proj", q, s)
+            if fused_o:
+                w, ws = layer["o_proj"]
+                h = fq.quant_mm(a[:, :Q_COLS], w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV)
+            else:
+                q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
+                h = self.mm(layer, "o_proj", q, s)
             q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
             gu = self.mm(layer, "gate_up_proj", q, s)
             q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)

@@ -176,3 +176,25 @@ def test_cpp_binding_declines_what_the_python_path_must_handle():
     assert f.silu_mul_quant(x, True, False) is None
     assert f.quant_per_token(x, True) is None
     assert f.launches() == 0
+
+
+def test_dynamic_quant_entry_validates_on_the_host():
+    L = _lib.lib()
+    assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, None) == _lib.OK
+    assert L.i8l_w8a8_mm_dynq_supported(1, 4096, 4096, None) == _lib.OK
+    assert L.i8l_w8a8_mm_dynq_supported(4, 2048, 6144, None) == _lib.UNSUPPORTED
+    assert "one step" in _lib.last_error()
+    c = _lib.CConfig(16, 32, 128, 16, 3, 1, 1)
+    assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, ctypes.byref(c)) == _lib.OK
+    c = _lib.CConfig(16, 32, 128, 8, 3, 1, 1)                  # two steps a wave: not built
+    assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, ctypes.byref(c)) == _lib.UNSUPPORTED
+    # argument errors come back before anything launches (no pointer is touched)
+    args = [None, 2048, _lib.BF16, 1, None, 1, 2048, None, 7, None, 0, None, 2048, _lib.BF16,
+            None, 4, 2048, 2048, None, None]
+    assert L.i8l_w8a8_mm_dynq(*args) == _lib.INVALID_ARG and "scale_b" in _lib.last_error()
+    args[8], args[1] = 2048, 1024                               # row stride below K
+    assert L.i8l_w8a8_mm_dynq(*args) == _lib.INVALID_ARG
+    args[1], args[2] = 2048, _lib.F32                           # fp32 activations
+    assert L.i8l_w8a8_mm_dynq(*args) == _lib.UNSUPPORTED
+    args[2], args[15] = _lib.BF16, 0                            # M == 0: nothing to do
+    assert L.i8l_w8a8_mm_dynq(*args) == _lib.OK
