@@ -1376,7 +1376,8 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {128, 256, 64, 2, 4, 4}, {128, 256, 128, 2, 4, 3},
                              {256, 128, 128, 2, 4, 3}, {128, 128, 64, 2, 2, 4},
                              {128, 128, 128, 2, 2, 4}, {64, 128, 128, 2, 2, 4},
-                             {64, 256, 128, 2, 4, 3}, {64, 128, 64, 2, 2, 6}};
+                             {64, 256, 128, 2, 4, 3}, {64, 128, 64, 2, 2, 6},
+                             {64, 128, 128, 2, 2, 6}};
 constexpr int kPipelined = 8;
 
 int dmap_index(const i8l_config& c) {
@@ -1623,6 +1624,7 @@ hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t ld
     case 9: return launch_dmap_t<64, 128, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 10: return launch_dmap_t<64, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
     case 11: return launch_dmap_t<64, 128, 64, 2, 2, 6>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 12: return launch_dmap_t<64, 128, 128, 2, 2, 6>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1783,8 +1785,8 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
   // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
   if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 64 && N >= 6144))) {
-    // very wide N has tiles enough for 128-token rows, which halve the weights' re-reads
-    if (N >= 16384)
+    // wide N has tiles enough for 128-token rows, which halve the weights' re-reads
+    if (N >= 16384 || (M > 128 && N >= 8192))
       *c = i8l_config{128, 128, 128, 4, 4 + kPipelined, 8, 1};
     else
       *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
