@@ -22,6 +22,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "i8l_common.h"
 
@@ -1289,6 +1290,23 @@ gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_
 // ------------------------------------------------------------------ host side
 namespace {
 
+// Opts a kernel in to `bytes` of dynamic LDS (needed above 64 KiB) on the current device,
+// once per device; `done` is the kernel's set of devices already opted in.  An unsupported
+// attribute is not fatal: the launch itself then reports the LDS overrun.
+void lds_opt_in(const void* kern, size_t bytes, std::atomic<uint64_t>& done) {
+  if (bytes <= 64 * 1024) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = -1;
+  }
+  const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return;
+  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  (void)hipGetLastError();
+  if (bit) done.fetch_or(bit, std::memory_order_relaxed);
+}
+
 struct StreamTile {
   int mt, nt, nc;
 };
@@ -1430,13 +1448,8 @@ hipError_t launch_wlds_k(const i8l_config& c, const int8_t* a, int64_t lda, cons
                          int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
   auto kern = gemm_wlds<MT, NC, KS, EK>;
   const size_t shm = wlds_lds_bytes(c, K);
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)kMaxLds);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, kMaxLds, lds_done);
   const int steps = (int)(K / ((int64_t)c.bk * c.warps));
   const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
   hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
@@ -1449,13 +1462,8 @@ hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t
                           const Epi& e, hipStream_t st) {
   auto kern = gemm_wlds1<MT, NC, KS, W, EK>;
   const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * (NC > 16 ? NC / 16 : 1) * 1024;
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set && shm > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)shm);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
   return hipGetLastError();
@@ -1541,14 +1549,8 @@ hipError_t launch_staged_t(const int8_t* a, int64_t lda, const int8_t* b, int64_
   auto kern = gemm_staged<BM, BN, BK, WM, WN>;
   const size_t shm = std::max<size_t>(2 * (size_t)(BM + BN) * BK,
                                       tile_epilogue_lds_bytes<BM, BN, WM, WN>());
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set && shm > 64 * 1024) {
-    // An unsupported attribute is not fatal: the launch itself reports an LDS overrun.
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)shm);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
   return hipGetLastError();
@@ -1560,13 +1562,8 @@ hipError_t launch_dma_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t l
   auto kern = gemm_dma<BM, BN, BK, WM, WN, S>;
   const size_t shm = std::max<size_t>((size_t)S * (BM + BN) * BK,
                                       tile_epilogue_lds_bytes<BM, BN, WM, WN>());
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set && shm > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)shm);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
   return hipGetLastError();
@@ -1597,13 +1594,8 @@ hipError_t launch_dmap_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t 
   auto kern = gemm_dmap<BM, BN, BK, WM, WN, S>;
   const size_t shm = std::max<size_t>((size_t)S * (BM + BN) * BK,
                                       tile_epilogue_lds_bytes<BM, BN, WM, WN>());
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set && shm > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)shm);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
   return hipGetLastError();
@@ -1690,13 +1682,8 @@ hipError_t launch_dq_k(const uint16_t* x, int64_t ldx, const int8_t* b, int64_t 
                        const Epi& e, float* sa_out, int precise, hipStream_t st) {
   auto kern = gemm_wlds1_dq<NC, KS, W, P, EK, DT>;
   const size_t shm = dq_lds_bytes(NC, KS, W);
-  static bool attr_set = false;  // opt in to more than 64 KiB of dynamic LDS, once
-  if (!attr_set && shm > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)shm);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const dim3 grid(e.N / NC, (e.M + 15) / 16);
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, x, ldx, b, ldb, e, sa_out, precise);
   return hipGetLastError();
