@@ -1395,7 +1395,8 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {256, 128, 128, 2, 4, 3}, {128, 128, 64, 2, 2, 4},
                              {128, 128, 128, 2, 2, 4}, {64, 128, 128, 2, 2, 4},
                              {64, 256, 128, 2, 4, 3}, {64, 128, 64, 2, 2, 6},
-                             {64, 128, 128, 2, 2, 6}};
+                             {64, 128, 128, 2, 2, 6}, {64, 64, 128, 2, 2, 4},
+                             {128, 64, 128, 2, 2, 4}};
 constexpr int kPipelined = 8;
 
 int dmap_index(const i8l_config& c) {
@@ -1617,6 +1618,8 @@ hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t ld
     case 10: return launch_dmap_t<64, 256, 128, 2, 4, 3>(a, lda, b, ldb, e, K, c.group_m, st);
     case 11: return launch_dmap_t<64, 128, 64, 2, 2, 6>(a, lda, b, ldb, e, K, c.group_m, st);
     case 12: return launch_dmap_t<64, 128, 128, 2, 2, 6>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 13: return launch_dmap_t<64, 64, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 14: return launch_dmap_t<128, 64, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1771,9 +1774,9 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   }
   // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
   // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
-  if (M <= 512 && N % 128 == 0 && K % 128 == 0 && (M > 128 || (M > 64 && N >= 6144))) {
-    // wide N has tiles enough for 128-token rows, which halve the weights' re-reads
-    if (N >= 16384 || (M > 128 && N >= 8192))
+  if (M > 64 && M <= 128 && N % 128 == 0 && K % 128 == 0 && N >= 6144) {
+    // very wide N has tiles enough for 128-token rows, which halve the weights' re-reads
+    if (N >= 16384)
       *c = i8l_config{128, 128, 128, 4, 4 + kPipelined, 8, 1};
     else
       *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
@@ -1804,6 +1807,20 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     c->warps = W;
     c->bk = 64 * W;
     c->stages = 1;
+    return;
+  }
+  // 129 to 1024 tokens: the largest of the 4-wave overlapped-ring tiles (128x128, 128x64,
+  // 64x128, 64x64) that still gives every CU a workgroup, else the smallest.  At these sizes
+  // the per-CU latency of the K loop, not the MFMA rate, sets the time, so more workgroups
+  // beat fewer re-reads.
+  if (M <= 1024 && N % 64 == 0 && K % 128 == 0) {
+    const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+    for (const auto& t : tiles)
+      if (N % t[1] == 0 && ((M + t[0] - 1) / t[0]) * (N / t[1]) >= 256) {
+        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8, 1};
+        return;
+      }
+    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8, 1};
     return;
   }
   // Prefill: direct-to-LDS macro tiles with the fragment reads overlapped with the MFMAs

@@ -52,7 +52,7 @@ DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
               (256, 128, 64, 8, 4), (128, 256, 64, 8, 4), (128, 256, 128, 8, 3),
               (256, 128, 128, 8, 3), (128, 128, 64, 4, 4), (128, 128, 128, 4, 4),
               (64, 128, 128, 4, 4), (64, 256, 128, 8, 3), (64, 128, 64, 4, 6),
-              (64, 128, 128, 4, 6)]
+              (64, 128, 128, 4, 6), (64, 64, 128, 4, 4), (128, 64, 128, 4, 4)]
 
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS

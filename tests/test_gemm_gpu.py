@@ -74,7 +74,8 @@ TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64,
            Config(256, 128, 128, 8, 11, 8), Config(128, 128, 64, 4, 12, 1),
            Config(128, 128, 128, 4, 12, 8), Config(64, 128, 128, 4, 12, 8),
            Config(64, 256, 128, 8, 11, 4), Config(64, 128, 64, 4, 14, 1),
-           Config(64, 128, 128, 4, 14, 8)]
+           Config(64, 128, 128, 4, 14, 8), Config(64, 64, 128, 4, 12, 8),
+           Config(128, 64, 128, 4, 12, 4)]
 
 
 @pytest.mark.parametrize("config", TILINGS, ids=lambda c: c.name.replace(" ", "_"))
