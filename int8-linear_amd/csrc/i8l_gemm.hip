@@ -1774,12 +1774,18 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   }
   // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
   // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
-  if (M > 64 && M <= 128 && N % 128 == 0 && K % 128 == 0 && N >= 6144) {
-    // very wide N has tiles enough for 128-token rows, which halve the weights' re-reads
-    if (N >= 16384)
-      *c = i8l_config{128, 128, 128, 4, 4 + kPipelined, 8, 1};
-    else
-      *c = i8l_config{64, 128, 128, 4, 4 + kPipelined, 4, 1};
+  // 129 to 1024 tokens, and from 33 tokens on wide N: the largest of the 4-wave overlapped-
+  // ring tiles (128x128, 128x64, 64x128, 64x64) that still gives every CU a workgroup, else
+  // the smallest.  At these sizes the per-CU latency of the K loop, not the MFMA rate, sets
+  // the time, so more workgroups beat fewer re-reads.
+  if (M <= 1024 && N % 64 == 0 && K % 128 == 0 && (M > 128 || (M > 32 && N >= 8192))) {
+    const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+    for (const auto& t : tiles)
+      if (N % t[1] == 0 && ((M + t[0] - 1) / t[0]) * (N / t[1]) >= 256) {
+        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8, 1};
+        return;
+      }
+    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8, 1};
     return;
   }
   // 17 to 128 tokens: weights through LDS in 32-token x 32-column tiles (several row
@@ -1807,20 +1813,6 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     c->warps = W;
     c->bk = 64 * W;
     c->stages = 1;
-    return;
-  }
-  // 129 to 1024 tokens: the largest of the 4-wave overlapped-ring tiles (128x128, 128x64,
-  // 64x128, 64x64) that still gives every CU a workgroup, else the smallest.  At these sizes
-  // the per-CU latency of the K loop, not the MFMA rate, sets the time, so more workgroups
-  // beat fewer re-reads.
-  if (M <= 1024 && N % 64 == 0 && K % 128 == 0) {
-    const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-    for (const auto& t : tiles)
-      if (N % t[1] == 0 && ((M + t[0] - 1) / t[0]) * (N / t[1]) >= 256) {
-        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8, 1};
-        return;
-      }
-    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8, 1};
     return;
   }
   // Prefill: direct-to-LDS macro tiles with the fragment reads overlapped with the MFMAs

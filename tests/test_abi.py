@@ -53,7 +53,9 @@ def test_default_config_regimes():
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
     assert default_config(300, 2048, 2048).stages >= 2
     mid = default_config(96, 12288, 2048)                   # 64-token overlapped-ring tiles
-    assert (mid.bm, mid.bn, mid.stages) == (64, 128, 12)
+    assert (mid.bm, mid.bn, mid.stages) == (64, 64, 12)
+    assert (default_config(512, 4096, 4096).bm, default_config(512, 4096, 4096).bn) == (128, 64)
+    assert (default_config(1024, 4096, 4096).bm, default_config(1024, 4096, 4096).bn) == (128, 128)
     assert default_config(400, 2048, 6144).bm == 64
     assert default_config(96, 4096, 2048).bn == 32          # narrower N: 32-column tiles
     for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
