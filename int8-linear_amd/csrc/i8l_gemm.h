@@ -1,0 +1,255 @@
+// Internal interface of the W8A8 GEMM: the epilogue and memory helpers shared by the decode
+// schedules (i8l_gemm_decode.hip), the prefill schedules (i8l_gemm_prefill.hip) and the
+// dispatch and C entry points (i8l_gemm.hip), and the host functions each exports.
+//
+//   out[m,n] = cast( f32(sum_k A[m,k] * B[k,n]) * sa[m|0] * sb[n|0] (+ f32(bias[n])) )
+//
+// Semantics follow the reference Triton kernel _w8a8_mm (AshrithaG/int8-linear,
+// int8_linear/kernel.py:63-124): exact int32 accumulation (94-103), then the epilogue in
+// fp32 in the order acc -> *sa -> *sb -> +bias (109-119) and one cast to the output dtype
+// (120); raw mode stores the int32 accumulator (106-107).  Every GEMM source is built with
+// -ffp-contract=off, so the epilogue is exactly that sequence of IEEE operations.
+#pragma once
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <atomic>
+
+#include "i8l_common.h"
+
+namespace i8l {
+
+// ------------------------------------------------------------------ epilogue
+struct Epi {
+  const float* sa;
+  const float* sb;
+  const void* bias;
+  void* out;
+  int64_t ldc;  // elements
+  int sa_per_row, sb_per_col, bias_dtype, out_dtype;
+  int M, N;
+};
+
+__device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) {
+  if (dt == I8L_BF16) return bf16_bits_to_f32(((const uint16_t*)bias)[n]);
+  if (dt == I8L_F16) return f16_bits_to_f32(((const uint16_t*)bias)[n]);
+  return ((const float*)bias)[n];
+}
+
+// Per-column epilogue operands of four consecutive output columns n..n+3.
+struct Cols4 {
+  float sb[4], bias[4];
+};
+
+// Epilogue kinds.  EK_ANY reads the output dtype, the bias dtype and the scale layout from
+// the Epi at run time; the other kinds fix them at compile time (bf16 out, per-column
+// scale_b, no bias or a bf16 bias), which leaves the decode kernels' critical path free of
+// the dtype branches: every CU starts a short kernel with a cold instruction cache, so each
+// taken branch into code not yet fetched waits for a fetch from L2.
+enum { EK_ANY = 0, EK_BF16 = 1, EK_BF16_BBF16 = 2 };
+template <int EK>
+__device__ __forceinline__ int epi_out(const Epi& e) { return EK == EK_ANY ? e.out_dtype : I8L_BF16; }
+template <int EK>
+__device__ __forceinline__ int epi_bias(const Epi& e) {
+  return EK == EK_ANY ? e.bias_dtype : EK == EK_BF16 ? I8L_DTYPE_NONE : I8L_BF16;
+}
+template <int EK>
+__device__ __forceinline__ bool epi_sb_per_col(const Epi& e) { return EK == EK_ANY ? e.sb_per_col != 0 : true; }
+
+// The kind a call can use (host side).
+inline int epi_kind(const Epi& e) {
+  if (e.out_dtype != I8L_BF16 || !e.sb_per_col) return EK_ANY;
+  if (e.bias_dtype == I8L_DTYPE_NONE) return EK_BF16;
+  if (e.bias_dtype == I8L_BF16) return EK_BF16_BBF16;
+  return EK_ANY;
+}
+
+// The epilogue operands of columns n..n+3 (n a multiple of 4): one vector load for the four
+// scales and one for the four bias values.  The fast schedules require 16-byte aligned
+// per-column scales and bias, so these loads are aligned; the dtype tests are uniform.
+template <int EK = EK_ANY>
+__device__ __forceinline__ Cols4 load_cols4(const Epi& e, int64_t n) {
+  Cols4 c;
+  const int od = epi_out<EK>(e), bd = epi_bias<EK>(e);
+  if (od == I8L_I32) return c;
+  if (epi_sb_per_col<EK>(e)) {
+    const float4 v = *(const float4*)(e.sb + n);
+    c.sb[0] = v.x, c.sb[1] = v.y, c.sb[2] = v.z, c.sb[3] = v.w;
+  } else {
+    const float v = e.sb[0];
+    c.sb[0] = c.sb[1] = c.sb[2] = c.sb[3] = v;
+  }
+  if (bd == I8L_F32) {
+    const float4 v = *(const float4*)((const float*)e.bias + n);
+    c.bias[0] = v.x, c.bias[1] = v.y, c.bias[2] = v.z, c.bias[3] = v.w;
+  } else if (bd == I8L_BF16 || bd == I8L_F16) {
+    const uint2 h = *(const uint2*)((const uint16_t*)e.bias + n);
+    const uint32_t w[4] = {h.x & 0xffffu, h.x >> 16, h.y & 0xffffu, h.y >> 16};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      c.bias[r] = bd == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
+  } else {
+    c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = 0.0f;
+  }
+  return c;
+}
+
+// Four consecutive output columns n..n+3 of row m (n a multiple of 4; the fast schedules
+// require a 16-byte aligned output with 16-byte aligned rows).
+template <int EK = EK_ANY>
+__device__ __forceinline__ float load_sa(const Epi& e, int64_t m) {
+  if (epi_out<EK>(e) == I8L_I32) return 0.0f;
+  return e.sa[m * (e.sa_per_row ? 1 : 0)];
+}
+
+template <int EK = EK_ANY>
+__device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i acc,
+                                        const Cols4& c, float sam) {
+  const int od = epi_out<EK>(e), bd = epi_bias<EK>(e);
+  if (od == I8L_I32) {
+    *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
+    return;
+  }
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = (float)acc[r];
+    v = v * sam;
+    v = v * c.sb[r];
+    if (bd != I8L_DTYPE_NONE) v = v + c.bias[r];
+    o[r] = v;
+  }
+  if (od == I8L_F32) {
+    *(float4*)((float*)e.out + m * e.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
+  } else {
+    uint32_t lo, hi;
+    if (od == I8L_BF16) {
+      lo = f32x2_to_bf16x2_bits(o[0], o[1]);
+      hi = f32x2_to_bf16x2_bits(o[2], o[3]);
+    } else {
+      lo = f32_to_f16_bits(o[0]) | ((uint32_t)f32_to_f16_bits(o[1]) << 16);
+      hi = f32_to_f16_bits(o[2]) | ((uint32_t)f32_to_f16_bits(o[3]) << 16);
+    }
+    *(uint2*)((uint16_t*)e.out + m * e.ldc + n) = make_uint2(lo, hi);
+  }
+}
+
+template <int EK = EK_ANY>
+__device__ __forceinline__ void store4c(const Epi& e, int64_t m, int64_t n, v4i acc,
+                                        const Cols4& c) {
+  store4s<EK>(e, m, n, acc, c, load_sa<EK>(e, m));
+}
+
+template <int EK = EK_ANY>
+__device__ __forceinline__ void store4(const Epi& e, int64_t m, int64_t n, v4i acc) {
+  store4c<EK>(e, m, n, acc, load_cols4<EK>(e, n));
+}
+
+__device__ __forceinline__ void store1(const Epi& e, int64_t m, int64_t n, int32_t acc) {
+  if (e.out_dtype == I8L_I32) {
+    ((int32_t*)e.out)[m * e.ldc + n] = acc;
+    return;
+  }
+  float v = (float)acc;
+  v = v * e.sa[e.sa_per_row ? m : 0];
+  v = v * e.sb[e.sb_per_col ? n : 0];
+  if (e.bias_dtype != I8L_DTYPE_NONE) v = v + load_bias(e.bias, e.bias_dtype, n);
+  if (e.out_dtype == I8L_F32)
+    ((float*)e.out)[m * e.ldc + n] = v;
+  else if (e.out_dtype == I8L_BF16)
+    ((uint16_t*)e.out)[m * e.ldc + n] = f32_to_bf16_bits(v);
+  else
+    ((uint16_t*)e.out)[m * e.ldc + n] = f32_to_f16_bits(v);
+}
+
+__device__ __forceinline__ v4i ld16(const int8_t* p) { return *(const v4i*)p; }
+// Weight bytes are read exactly once per call: stream them past the caches.
+__device__ __forceinline__ v4i ld16_stream(const int8_t* p) {
+  return __builtin_nontemporal_load((const v4i*)p);
+}
+
+// Column tile of a decode workgroup.  The dispatcher deals workgroups to the 8 XCDs
+// round-robin by linear id; with a multiple of 8 column tiles per row, XCD x is given the
+// contiguous column range [x, x+1) * gridDim.x/8, so the output lines (and the L2 lines
+// they are assembled in) are written from one XCD rather than in pieces from eight.
+__device__ __forceinline__ int64_t xcd_col_tile() {
+  const int gx = gridDim.x, bx = blockIdx.x;
+  return gx % 8 == 0 ? (int64_t)(bx % 8) * (gx / 8) + bx / 8 : (int64_t)bx;
+}
+
+// ------------------------------------------------------------------ shared limits
+// Decode register-streaming tiles: K steps loaded U at a time (U = stream_unroll).
+__host__ __device__ constexpr int stream_unroll(int mt, int nt) { return mt * nt >= 4 ? 2 : 4; }
+// Largest workgroup whose waves keep the double-buffered fragments in registers.
+__host__ __device__ constexpr int stream_max_threads(int mt, int nt) {
+  return 2 * stream_unroll(mt, nt) * (mt + nt) * 4 + mt * nt * 4 <= 80 ? 1024 : 512;
+}
+
+// Weights-through-LDS decode tiles: the largest workgroup (threads) of a tile.
+__host__ __device__ constexpr int wlds_bound(int mt, int ks) { return mt * ks <= 6 ? 1024 : 512; }
+// Whether the multi-step kernel's registers fit: two sets of activation fragments, the
+// weight fragments of a step and the accumulators, in VGPRs (64 x 4 bytes each).
+__host__ __device__ constexpr bool wlds_multi_fits(int mt, int nc, int ks) {
+  return 8 * ks * mt + 4 * ks * (nc > 16 ? nc / 16 : 1) + 4 * mt * (nc > 16 ? nc / 16 : 1) <= 176;
+}
+
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU, bytes
+constexpr int kPipelined = 8;           // the overlapped-ring configs' stages: ring depth + 8
+
+// Workgroup barrier without a memory fence: LDS accesses are ordered around it by the
+// compiler-level fences; waits for outstanding memory are issued explicitly where needed.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------------------------ host helpers
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+inline int elt_size(int dt) { return dt == I8L_BF16 || dt == I8L_F16 ? 2 : 4; }
+
+// Opts a kernel in to `bytes` of dynamic LDS (needed above 64 KiB) on the current device,
+// once per device; `done` is the kernel's set of devices already opted in.  An unsupported
+// attribute is not fatal: the launch itself then reports the LDS overrun.
+inline void lds_opt_in(const void* kern, size_t bytes, std::atomic<uint64_t>& done) {
+  if (bytes <= 64 * 1024) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = -1;
+  }
+  const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return;
+  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  (void)hipGetLastError();
+  if (bit) done.fetch_or(bit, std::memory_order_relaxed);
+}
+
+// ------------------------------------------------------------------ schedules (host side)
+// Decode (i8l_gemm_decode.hip).
+bool stream_ok(const i8l_config& c);
+bool wlds_ok(const i8l_config& c, int64_t K);
+hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int K, hipStream_t st);
+hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                       int64_t ldb, const Epi& e, int64_t K, hipStream_t st);
+bool dq_ok(const i8l_config& c, int64_t K);
+bool default_dq_config(int64_t N, int64_t K, i8l_config* c);
+hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
+                     const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
+                     hipStream_t st);
+// Prefill (i8l_gemm_prefill.hip): the index of a config among the built tiles, or -1.
+int staged_index(const i8l_config& c);
+int dma_index(const i8l_config& c);
+int dmap_index(const i8l_config& c);
+hipError_t launch_staged(int idx, const i8l_config& c, const int8_t* a, int64_t lda,
+                         const int8_t* b, int64_t ldb, const Epi& e, int K, hipStream_t st);
+hipError_t launch_dma(int idx, const i8l_config& c, const int8_t* a, int64_t lda,
+                      const int8_t* b, int64_t ldb, const Epi& e, int K, hipStream_t st);
+hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t lda,
+                       const int8_t* b, int64_t ldb, const Epi& e, int K, hipStream_t st);
+
+}  // namespace i8l

@@ -1,0 +1,867 @@
+// Decode schedules of the W8A8 GEMM (M <= 128 tokens), their tile tables and launchers:
+//  * stream: weights streamed from HBM straight into MFMA operand registers;
+//  * wlds / wlds1: weights copied through LDS with direct-to-LDS loads, K split over the
+//    waves, one or several steps a wave;
+//  * wlds1_dq: wlds1 with the per-token activation quantizer folded in.
+// v_mfma_i32_16x16x64_i8 with the weight fragment as srcA and the activations as srcB.
+#include "i8l_gemm.h"
+
+namespace i8l {
+
+// ------------------------------------------------------------------ stream schedule
+// Workgroup = W waves on the same 16*NT output columns and 16*MT tokens; wave w owns the
+// contiguous K slice [w*ks*64, (w+1)*ks*64).  Lane l of a wave loads, per 64-byte K step,
+// 16 bytes of weight row (n0 + 16t + l%16) at K offset 16*(l/16), and the same 16 bytes
+// of K for token (m0 + 16i + l%16): both MFMA operands then hold the same K positions,
+// so the product is the exact dot product whatever order the unit sums them in.
+// Accumulator lane l, register r of fragment (i,t) is out[m0+16i+l%16][n0+16t+4*(l/16)+r].
+// K steps are loaded U at a time, one group ahead of the MFMAs consuming the previous one.
+
+// NC (16, 8 or 4) output columns per MFMA tile: with NC < 16, MFMA rows i and i+NC read
+// the same weight row (the loads coalesce, so HBM traffic is unchanged) and only rows
+// below NC are stored.  Narrow tiles give narrow-N shapes more workgroups.
+template <int MT, int NT, int U, int NC>
+__global__ void __launch_bounds__(stream_max_threads(MT, NT))
+gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
+            int64_t ldb, Epi e, int ks) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = blockDim.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * (NC * NT);
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kbeg = (int64_t)wave * ks * 64 + grp * 16;
+
+  const int8_t* bp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) bp[t] = B + (n0 + NC * t + r16 % NC) * ldb + kbeg;
+  const int8_t* ap[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int64_t m = m0 + 16 * i + r16;
+    ap[i] = A + (m < e.M ? m : 0) * lda + kbeg;
+  }
+
+  v4i acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = v4i{0, 0, 0, 0};
+
+  // Two register buffers of U steps each, used in turn (no copies between them, so the
+  // wait before each group's MFMAs covers exactly that group's loads).  Padding token
+  // rows load row 0's bytes: their output columns are computed but never stored.
+  v4i b0[U][NT], a0[U][MT], b1[U][NT], a1[U][MT];
+  auto load = [&](v4i (&bb)[U][NT], v4i (&aa)[U][MT], int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) bb[u][t] = ld16_stream(bp[t] + (s + u) * 64);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) aa[u][i] = ld16(ap[i] + (s + u) * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any MFMA waits
+  };
+  auto mma = [&](const v4i (&bb)[U][NT], const v4i (&aa)[U][MT]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bb[u][t], aa[u][i], acc[i][t], 0, 0, 0);
+  };
+  // Steady state: every load unconditional, so at each wait exactly the group after the
+  // one being consumed is still in flight on every path.
+  const int G = ks / U;  // groups of U steps
+  load(b0, a0, 0);
+  // The wave that stores fragment f (f % W == wave) loads its scales and bias now, behind
+  // the first weight group, so their latency is hidden by the main loop.
+  constexpr int F = MT * NT;
+  Cols4 cl0;
+  float sa0 = 0.0f;
+  if (wave < F && 4 * grp < NC) {
+    const int i = wave / NT, t = wave % NT;
+    const int64_t m = m0 + 16 * i + r16;
+    cl0 = load_cols4(e, n0 + NC * t + 4 * grp);
+    sa0 = load_sa(e, m < e.M ? m : 0);
+  }
+  int g = 0;
+  for (; g + 2 < G; g += 2) {
+    load(b1, a1, (g + 1) * U);
+    mma(b0, a0);
+    load(b0, a0, (g + 2) * U);
+    mma(b1, a1);
+  }
+  if (G - g == 2) {
+    load(b1, a1, (g + 1) * U);
+    mma(b0, a0);
+    mma(b1, a1);
+  } else {
+    mma(b0, a0);
+  }
+
+  // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
+  extern __shared__ v4i red[];  // [W][MT*NT][64]
+  if (W > 1) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) red[(wave * F + i * NT + t) * 64 + lane] = acc[i][t];
+    __syncthreads();
+  }
+  for (int f = wave; f < F; f += W) {
+    v4i s;
+    if (W > 1) {
+      s = red[f * 64 + lane];
+      for (int w = 1; w < W; ++w) s += red[(w * F + f) * 64 + lane];
+    } else {
+      // W == 1: the fragment is this wave's own accumulator
+      s = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          if (i * NT + t == f) s = acc[i][t];
+    }
+    const int i = f / NT, t = f % NT;
+    const int64_t m = m0 + 16 * i + r16;
+    if (m < e.M && 4 * grp < NC) {
+      if (f == wave)
+        store4s(e, m, n0 + NC * t + 4 * grp, s, cl0, sa0);
+      else
+        store4(e, m, n0 + NC * t + 4 * grp, s);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ weights-through-LDS schedule
+// Decode tile of 16*MT tokens x NC columns (NC = 16, 8 or 4).  Each wave owns one contiguous
+// K slice of `steps` steps of S = 64*KS bytes.  Per step it copies its NC x S weight bytes
+// into its own LDS buffer with global_load_lds_dwordx4: one instruction moves 1 KiB, whole
+// row segments of S bytes, so HBM sees full cache lines (the MFMA operand layout would read
+// 16 rows x 64 bytes per instruction instead).  LDS row r holds 16-byte chunk c at slot
+// c ^ (r & SWM), so the MFMA-layout reads (16 rows, one chunk each) spread over the banks.
+// The activations of the next step are loaded into registers while the current step
+// multiplies.  A wave only reads its own buffers, so its own vmcnt wait is the only
+// synchronisation until the cross-wave sum of the int32 partials.
+// With NC < 16, MFMA rows i and i+NC read the same weight row and only rows below NC are
+// stored.  Token rows past M read row 0 and are never stored.
+
+// s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
+// no LDS read of the DMA'd data is scheduled above the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_wlds() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) int8_t lds_i8_t;
+
+template <int MT, int NC, int KS, int EK>
+__global__ void __launch_bounds__(wlds_bound(MT, KS))
+gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
+          Epi e, int steps, int nbuf) {
+  constexpr int S = 64 * KS;                 // K bytes per row per step
+  constexpr int CPR = S / 16;                // 16-byte chunks per row per step
+  // The swizzle XORs a slot with (row & SWM); SWM + 1 is a power of two dividing CPR, so
+  // every slot maps into the same row's [0, CPR) and no address leaves the row's slice.
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;                 // weight bytes per wave per step
+  constexpr int NI = SB / 1024;              // DMA instructions per wave per step
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int AL = MT * KS;                // activation loads per lane per step
+  constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
+  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int FR = MT * NF;                // output fragments, numbered i * NF + f
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  // wave-uniform values live in scalar registers: the per-lane address work before the first
+  // load is then a few 32-bit operations
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)wave * steps * S;
+  int8_t* wbuf = lds + (size_t)wave * nbuf * SB;
+
+  // DMA sources of this lane: instruction t writes LDS bytes [t*1024, t*1024+1024) of the
+  // step buffer, lane l the 16 bytes at +16*l, which is row o / S, slot (o % S) / 16.
+  // Rows of a tile are < 32 apart, so their offsets fit 32 bits.
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  const int8_t* gsrc[NI];
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    gsrc[t] = Bw + (r * ldb32 + 16 * c);
+  }
+  // Token rows past M read the tile's first row (always valid); they are never stored.
+  const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
+  const int lda32 = (int)lda;
+  const int8_t* ap[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = 16 * i + r16;
+    ap[i] = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
+  }
+  // MFMA-layout read offsets of one step: fragment f's row br, chunk 4s + grp
+  int rofs[KS][NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) rofs[s][f] = br * S + 16 * ((4 * s + grp) ^ (br & SWM));
+  }
+
+  v4i acc[MT][NF];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
+
+  v4i a0[KS][MT], a1[KS][MT];
+  // `fenced`: nothing of the previous step's MFMA work moves below the start of the issue,
+  // so the LDS reads of the buffer the step may overwrite have completed, and the loads go
+  // out before anything after them.  A single-step wave needs neither, and leaving the
+  // compiler free to interleave the address arithmetic with the loads issues them sooner.
+  auto issue = [&](v4i (&aa)[KS][MT], int step, bool fenced) {
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+    lds_i8_t* dst = (lds_i8_t*)(wbuf + (step % nbuf) * SB);
+    const int64_t ko = (int64_t)step * S;
+#pragma unroll
+    for (int t = 0; t < NI; ++t)
+      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) aa[s][i] = ld16(ap[i] + ko + 64 * s);
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](const v4i (&aa)[KS][MT], int step) {
+    const int8_t* base = wbuf + (step % nbuf) * SB;
+    v4i b[KS][NF];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) b[s][f] = *(const v4i*)(base + rofs[s][f]);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], aa[s][i], acc[i][f], 0, 0, 0);
+  };
+
+  issue(a0, 0, steps > 1);
+  // The wave that stores fragment fr (fr % W == wave) loads its epilogue operands now,
+  // behind the first step, so their latency hides under the main loop.
+  Cols4 cl0;
+  float sa0 = 0.0f;
+  if (wave < FR && 4 * grp < NCF) {
+    const int64_t m = m0 + 16 * (wave / NF) + r16;
+    cl0 = load_cols4<EK>(e, n0 + NCF * (wave % NF) + 4 * grp);
+    sa0 = load_sa<EK>(e, m < e.M ? m : 0);
+  }
+  // Steady state: every step's loads are issued before the wait for the previous step, and
+  // the wait leaves exactly one step's loads outstanding.  The LDS reads of a step complete
+  // before its MFMAs, so its buffer is free when the step two later overwrites it.
+  int i = 0;
+  for (; i + 2 < steps; i += 2) {
+    issue(a1, i + 1, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a0, i);
+    issue(a0, i + 2, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a1, i + 1);
+  }
+  if (steps - i == 2) {
+    issue(a1, i + 1, true);
+    wait_vmcnt_wlds<NI + AL>();
+    compute(a0, i);
+    wait_vmcnt_wlds<0>();
+    compute(a1, i + 1);
+  } else {
+    wait_vmcnt_wlds<0>();
+    compute(a0, i);
+  }
+
+  // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
+  v4i* red = (v4i*)(lds + (size_t)W * nbuf * SB);  // [W][FR][64]
+  if (W > 1) {
+#pragma unroll
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) red[(wave * FR + q * NF + f) * 64 + lane] = acc[q][f];
+    __syncthreads();
+  }
+  for (int fr = wave; fr < FR; fr += W) {
+    v4i sum;
+    if (W > 1) {
+      sum = red[fr * 64 + lane];
+      for (int w = 1; w < W; ++w) sum += red[(w * FR + fr) * 64 + lane];
+    } else {
+      sum = acc[0][0];
+#pragma unroll
+      for (int q = 0; q < MT; ++q)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          if (q * NF + f == fr) sum = acc[q][f];
+    }
+    const int64_t m = m0 + 16 * (fr / NF) + r16;
+    const int64_t n = n0 + NCF * (fr % NF) + 4 * grp;
+    if (m < e.M && 4 * grp < NCF) {
+      if (fr == wave)
+        store4s<EK>(e, m, n, sum, cl0, sa0);
+      else
+        store4<EK>(e, m, n, sum);
+    }
+  }
+}
+
+// The same tile when every wave's K slice is a single step (K == W * 64 * KS), with the
+// wave count and the epilogue kind fixed at compile time: the path from the first load to
+// the last store is straight-line code apart from the wave-uniform test of which waves
+// store, which matters in a kernel this short (see EK_ANY).
+template <int MT, int NC, int KS, int W, int EK>
+__global__ void __launch_bounds__(64 * W)
+gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
+           Epi e) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;
+  constexpr int NI = SB / 1024;
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
+  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int FR = MT * NF;                // output fragments of the tile
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  static_assert(FR <= W, "every fragment needs a storing wave");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)wave * S;
+  int8_t* wbuf = lds + (size_t)wave * SB;
+
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  lds_i8_t* dst = (lds_i8_t*)wbuf;
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                     16, 0, 0);
+  }
+  const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
+  const int lda32 = (int)lda;
+  v4i a[KS][MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = 16 * i + r16;
+    const int8_t* ap = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s][i] = ld16(ap + 64 * s);
+  }
+  // Wave w < FR stores fragment (token block w / NF, column block w % NF) and loads its
+  // epilogue operands now, behind the tile; lanes past NCF columns load a valid neighbour
+  // and never store.
+  Cols4 cl;
+  float sam = 0.0f;
+  const int64_t mrow = m0 + 16 * (wave / NF) + r16;
+  const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+  if (wave < FR) {
+    cl = load_cols4<EK>(e, ncol);
+    sam = load_sa<EK>(e, mrow < e.M ? mrow : m0);
+  }
+  wait_vmcnt_wlds<0>();
+  v4i b[KS][NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      b[s][f] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+  }
+  v4i acc[MT][NF];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s][i], acc[i][f], 0, 0, 0);
+
+  // cross-wave sum (exact int32), then the storing waves apply the epilogue
+  v4i* red = (v4i*)(lds + (size_t)W * SB);  // [W][FR][64]
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) red[(wave * FR + i * NF + f) * 64 + lane] = acc[i][f];
+  __syncthreads();
+  if (wave < FR) {
+    v4i sum = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[(w * FR + wave) * 64 + lane];
+    if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
+  }
+}
+
+// ------------------------------------------------------------------ dynamic-quant decode
+// gemm_wlds1 with the per-token activation quantizer folded in, for one 16-token row block.
+// A arrives as the bf16/fp16 X [M, K] that quant_per_token would quantize; each wave
+// quantizes its own K slice of the block's valid rows, with each row's absmax combined
+// across the lanes holding it and then across the waves.  The arithmetic is the quantizer
+// kernel's (absmax of |x|, scale = absmax/127, codes = rint(x * 127/absmax) clamped to
+// [-128, 127]; reference fused_quant.py:41-53), so the output equals quant_per_token followed
+// by w8a8_mm bit for bit, from one kernel instead of two.
+//
+// Every column tile repeats the row work, so the layout keeps it proportional to the valid
+// rows: a wave reads its slice as 16-byte chunks of 8 values, CH = S/8 chunks a row and
+// 64/CH rows a pass over the lanes, quantizes them, and writes the codes to an LDS tile of
+// 16 rows x S bytes, from which the MFMA fragments are read (rows past M read as zero).
+template <int NC, int KS, int W, int P, int EK, int DT>
+__global__ void __launch_bounds__(64 * W)
+gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ B,
+              int64_t ldb, Epi e, float* __restrict__ sa_out, int precise) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;
+  constexpr int NI = SB / 1024;
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int NCF = NC < 16 ? NC : 16;
+  constexpr int NF = NC / NCF;
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  static_assert(NF <= W, "every fragment needs a storing wave");
+  constexpr int CH = S / 8;                  // 8-value chunks of a row in a wave's slice
+  constexpr int RPP = 64 / CH;               // rows a pass covers
+  static_assert(RPP * CH == 64 && 16 % RPP == 0, "rows must split over the lanes");
+  static_assert(P >= 1 && P * RPP <= 16, "P passes of RPP rows cover the block's valid rows");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * 16;
+  // valid rows of the block; the host picks P = ceil(mb / RPP), so every pass is needed and
+  // the code has no skipped (taken-branch) passes
+  const int mb = (int)min((int64_t)16, (int64_t)e.M - m0);
+  const int64_t kw = (int64_t)wave * S;
+  int8_t* wbuf = lds + (size_t)wave * SB;
+  v4i* red = (v4i*)(lds + (size_t)W * SB);                          // [W][NF][64]
+  float* rmax = (float*)(lds + (size_t)W * SB + (size_t)W * NF * 1024);  // [W][16]
+  float* scl = rmax + W * 16;               // [W][16]: each wave's copy of the row scales
+  int8_t* abuf = lds + (size_t)W * SB + (size_t)W * NF * 1024 + (size_t)W * 128 + wave * 16 * S;
+
+  // The activations are requested first and waited for alone: the quantizer work below
+  // then runs while the weights' DMA is still in flight.
+  // pass p: lane l holds chunk l % CH of row p*RPP + l/CH (rows past M are not read)
+  const int crow = lane / CH, cchunk = lane % CH;
+  uint4 xr[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    xr[p] = uint4{0, 0, 0, 0};
+    const int r = p * RPP + crow;
+    if (r < mb) xr[p] = *(const uint4*)(X + (m0 + r) * ldx + kw + 8 * cchunk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int ldb32 = (int)ldb;
+  lds_i8_t* dst = (lds_i8_t*)wbuf;
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                     16, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt_wlds<NI>();  // vector loads complete in issue order: the activations are in
+
+  auto elem = [&](const uint4& v, int k) -> float {
+    const uint32_t w32 = k < 4 ? (k < 2 ? v.x : v.y) : (k < 6 ? v.z : v.w);
+    return act_to_f32<DT>((k & 1) ? (w32 >> 16) : (w32 & 0xffffu));
+  };
+  // absmax of each valid row's slice: a lane's chunk, then the CH lanes of the row
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(elem(xr[p], k)));
+    am = group_max<CH>(am);
+    if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
+  }
+  __syncthreads();
+  auto row_scale = [&](int r, float& scale, float& inv) {
+    float absmax = rmax[r];
+#pragma unroll
+    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + r]);
+    const float s_div = absmax / 127.0f;
+    const float i_div = absmax == 0.0f ? 0.0f : 127.0f / absmax;
+    const float s_rcp = absmax * (1.0f / 127.0f);
+    const float i_rcp = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
+    scale = precise ? s_div : s_rcp;
+    inv = precise ? i_div : i_rcp;
+  };
+  // codes of each valid chunk into the wave's LDS tile (row pitch S bytes)
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = p * RPP + crow;
+    if (r < mb) {
+      float scale, inv;
+      row_scale(r, scale, inv);
+      uint32_t word[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float v = __builtin_rintf(elem(xr[p], 4 * q + b) * inv);
+          v = fminf(fmaxf(v, -128.0f), 127.0f);
+          packed |= ((uint32_t)(int)v & 0xffu) << (8 * b);
+        }
+        word[q] = packed;
+      }
+      *(uint2*)(abuf + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
+      if (cchunk == 0) {
+        scl[wave * 16 + r] = scale;
+        if (sa_out != nullptr && blockIdx.x == 0 && wave == 0) sa_out[m0 + r] = scale;
+      }
+    }
+  }
+  Cols4 cl;
+  const int64_t mrow = m0 + r16;
+  const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+  if (wave < NF) cl = load_cols4<EK>(e, ncol);
+  wait_vmcnt_wlds<0>();  // the weights, and the epilogue operands
+  // the wave's own LDS writes are complete before its reads below (LDS is in order per wave)
+  v4i a[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    a[s] = r16 < mb ? *(const v4i*)(abuf + r16 * S + 64 * s + 16 * grp) : v4i{0, 0, 0, 0};
+
+  v4i b[KS][NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int br = NCF * f + r16 % NCF;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      b[s][f] = *(const v4i*)(wbuf + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+  }
+  v4i acc[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) acc[f] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s], acc[f], 0, 0, 0);
+
+#pragma unroll
+  for (int f = 0; f < NF; ++f) red[(wave * NF + f) * 64 + lane] = acc[f];
+  __syncthreads();
+  if (wave < NF) {
+    v4i sum = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[(w * NF + wave) * 64 + lane];
+    // this wave's own scale of row r16 (written above by this wave: LDS is in order)
+    if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, scl[wave * 16 + r16]);
+  }
+}
+
+// ------------------------------------------------------------------ host side
+struct StreamTile {
+  int mt, nt, nc;
+};
+
+// The tiles this library is built with.
+// (MT, NT, NC): bm = 16*MT tokens, bn = NC*NT columns.  NC < 16 only with NT == 1, so bn
+// names the tile unambiguously.
+constexpr StreamTile kStream[] = {{1, 1, 16}, {2, 1, 16}, {4, 1, 16}, {8, 1, 16}, {1, 2, 16},
+                                  {2, 2, 16}, {4, 2, 16}, {1, 1, 8},  {2, 1, 8},  {1, 1, 4}};
+
+bool stream_ok(const i8l_config& c) {
+  if (c.stages != 1 || c.split_k != 1 || c.bm % 16) return false;
+  if (c.warps < 1 || c.bk != 64 * c.warps) return false;
+  for (auto t : kStream)
+    if (t.mt * 16 == c.bm && t.nt * t.nc == c.bn) {
+      const int f = t.mt * t.nt;
+      return c.warps * 64 <= stream_max_threads(t.mt, t.nt) &&
+             (c.warps == 1 || c.warps * f * 1024 <= 96 * 1024);
+    }
+  return false;
+}
+
+// Weights-through-LDS decode tiles (MT, NC, KS): bm = 16*MT, bn = NC, bk = 64*KS bytes of K
+// per wave step; the config's `stages` is 3 and K must split into warps x steps x bk.
+struct WldsTile {
+  int mt, nc, ks;
+};
+constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1, 8, 2},
+                              {1, 8, 4},  {1, 8, 6},  {1, 8, 8},  {1, 4, 4},  {1, 4, 8},
+                              {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4},  {4, 16, 2},
+                              {4, 16, 4}, {4, 8, 2},  {4, 8, 4},  {8, 16, 2}, {8, 8, 2},
+                              {1, 32, 2}, {1, 32, 4}, {2, 32, 2}, {2, 32, 4}, {4, 32, 2},
+                              {4, 32, 4}};
+
+size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
+  const int64_t steps = K / ((int64_t)c.bk * c.warps);
+  const int nbuf = steps > 1 ? 2 : 1;
+  const int nf = c.bn > 16 ? c.bn / 16 : 1;  // 16-column fragments a wave reduces
+  return (size_t)c.warps * nbuf * c.bn * c.bk + (size_t)c.warps * (c.bm / 16) * nf * 1024;
+}
+
+bool wlds1_built(int mt, int nc, int W, int ks);
+
+bool wlds_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 3 || c.split_k != 1 || c.bn > 32 || c.warps < 1 || c.warps > 16) return false;
+  bool built = false;
+  for (auto t : kWlds)
+    if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
+        c.warps * 64 <= wlds_bound(t.mt, t.ks))
+      built = true;
+  if (!built || K <= 0 || K % ((int64_t)c.bk * c.warps)) return false;
+  const bool one_step = K == (int64_t)c.bk * c.warps &&
+                        wlds1_built(c.bm / 16, c.bn, c.warps, c.bk / 64);
+  if (!one_step && !wlds_multi_fits(c.bm / 16, c.bn, c.bk / 64)) return false;
+  return wlds_lds_bytes(c, K) <= kMaxLds;
+}
+
+template <int MT, int NT, int NC>
+hipError_t launch_stream_u(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                           const Epi& e, int W, int ks, hipStream_t st) {
+  const dim3 grid(e.N / (NC * NT), (e.M + 16 * MT - 1) / (16 * MT));
+  const size_t shm = W > 1 ? (size_t)W * MT * NT * 1024 : 0;
+  constexpr int UMAX = stream_unroll(MT, NT);
+  if (UMAX == 4 && ks % 4 == 0)
+    hipLaunchKernelGGL((gemm_stream<MT, NT, UMAX, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+  else if (ks % 2 == 0)
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 2, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+  else
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 1, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+  return hipGetLastError();
+}
+
+template <int MT, int NC, int KS, int EK>
+hipError_t launch_wlds_k(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  auto kern = gemm_wlds<MT, NC, KS, EK>;
+  const size_t shm = wlds_lds_bytes(c, K);
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, kMaxLds, lds_done);
+  const int steps = (int)(K / ((int64_t)c.bk * c.warps));
+  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
+                     steps > 1 ? 2 : 1);
+  return hipGetLastError();
+}
+
+template <int MT, int NC, int KS, int W, int EK>
+hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  auto kern = gemm_wlds1<MT, NC, KS, W, EK>;
+  const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * (NC > 16 ? NC / 16 : 1) * 1024;
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
+  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
+  return hipGetLastError();
+}
+
+// Single-step launches for the (waves, step) pairs built: K = 64 * KS * W.
+template <int MT, int NC, int KS, int EK>
+hipError_t launch_wlds1_w(int W, const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  constexpr int FR = MT * (NC > 16 ? NC / 16 : 1);  // fragments: one storing wave each
+  if constexpr (KS <= 8) {
+    if constexpr (FR <= 4)
+      if (W == 4 && (KS == 4 || KS == 8)) return launch_wlds1_k<MT, NC, KS, 4, EK>(a, lda, b, ldb, e, st);
+    if constexpr (FR <= 8)
+      if (W == 8) return launch_wlds1_k<MT, NC, KS, 8, EK>(a, lda, b, ldb, e, st);
+    if constexpr (wlds_bound(MT, KS) >= 1024 && KS <= 6)
+      if (W == 16) return launch_wlds1_k<MT, NC, KS, 16, EK>(a, lda, b, ldb, e, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+bool wlds1_built(int mt, int nc, int W, int ks) {
+  const int fr = mt * (nc > 16 ? nc / 16 : 1);
+  return ks <= 8 && ((W == 4 && fr <= 4 && (ks == 4 || ks == 8)) || (W == 8 && fr <= 8) ||
+                     (W == 16 && ks <= 6 && wlds_bound(mt, ks) >= 1024));
+}
+
+template <int MT, int NC, int KS>
+hipError_t launch_wlds_t(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  if (K == (int64_t)c.bk * c.warps && wlds1_built(MT, NC, c.warps, KS)) {
+    switch (epi_kind(e)) {
+      case EK_BF16: return launch_wlds1_w<MT, NC, KS, EK_BF16>(c.warps, a, lda, b, ldb, e, st);
+      case EK_BF16_BBF16:
+        return launch_wlds1_w<MT, NC, KS, EK_BF16_BBF16>(c.warps, a, lda, b, ldb, e, st);
+      default: return launch_wlds1_w<MT, NC, KS, EK_ANY>(c.warps, a, lda, b, ldb, e, st);
+    }
+  }
+  if constexpr (wlds_multi_fits(MT, NC, KS)) {
+    switch (epi_kind(e)) {
+      case EK_BF16: return launch_wlds_k<MT, NC, KS, EK_BF16>(c, a, lda, b, ldb, e, K, st);
+      case EK_BF16_BBF16:
+        return launch_wlds_k<MT, NC, KS, EK_BF16_BBF16>(c, a, lda, b, ldb, e, K, st);
+      default: return launch_wlds_k<MT, NC, KS, EK_ANY>(c, a, lda, b, ldb, e, K, st);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                       int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  const int mt = c.bm / 16, nc = c.bn, ks = c.bk / 64;
+#define I8L_WLDS(MT_, NC_, KS_)                                                             \
+  if (mt == MT_ && nc == NC_ && ks == KS_) return launch_wlds_t<MT_, NC_, KS_>(c, a, lda, b, ldb, e, K, st);
+  I8L_WLDS(1, 16, 2) I8L_WLDS(1, 16, 4) I8L_WLDS(1, 16, 6) I8L_WLDS(1, 16, 8)
+  I8L_WLDS(1, 8, 2) I8L_WLDS(1, 8, 4) I8L_WLDS(1, 8, 6) I8L_WLDS(1, 8, 8)
+  I8L_WLDS(1, 4, 4) I8L_WLDS(1, 4, 8)
+  I8L_WLDS(2, 16, 2) I8L_WLDS(2, 16, 4) I8L_WLDS(2, 8, 2) I8L_WLDS(2, 8, 4)
+  I8L_WLDS(4, 16, 2) I8L_WLDS(4, 16, 4) I8L_WLDS(4, 8, 2) I8L_WLDS(4, 8, 4)
+  I8L_WLDS(8, 16, 2) I8L_WLDS(8, 8, 2)
+  I8L_WLDS(1, 32, 2) I8L_WLDS(1, 32, 4) I8L_WLDS(2, 32, 2) I8L_WLDS(2, 32, 4)
+  I8L_WLDS(4, 32, 2) I8L_WLDS(4, 32, 4)
+#undef I8L_WLDS
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                         int64_t ldb, const Epi& e, int K, hipStream_t st) {
+  const int mt = c.bm / 16, bn = c.bn, W = c.warps, ks = K / (64 * W);
+#define I8L_STREAM(MT_, NT_, NC_)                                                          \
+  if (mt == MT_ && bn == NT_ * NC_)                                                       \
+    return launch_stream_u<MT_, NT_, NC_>(a, lda, b, ldb, e, W, ks, st);
+  I8L_STREAM(1, 1, 16) I8L_STREAM(2, 1, 16) I8L_STREAM(4, 1, 16) I8L_STREAM(8, 1, 16)
+  I8L_STREAM(1, 2, 16) I8L_STREAM(2, 2, 16) I8L_STREAM(4, 2, 16)
+  I8L_STREAM(1, 1, 8) I8L_STREAM(2, 1, 8) I8L_STREAM(1, 1, 4)
+#undef I8L_STREAM
+  return hipErrorInvalidValue;
+}
+
+// Dynamic-quant decode tiles (gemm_wlds1_dq, one 16-token row block): (NC, KS, W) with
+// K == 64 * KS * W.  The config's bm is 16 and its stages 3, as for gemm_wlds1.
+struct DqTile {
+  int nc, ks, w;
+};
+constexpr DqTile kDq[] = {{8, 2, 16}, {16, 2, 16}, {32, 2, 16}, {8, 4, 16}, {16, 4, 16}};
+
+size_t dq_lds_bytes(int nc, int ks, int W) {
+  const int nf = nc > 16 ? nc / 16 : 1;
+  // weights, the cross-wave sums, the row maxima and scales, the 16-row code tiles
+  return (size_t)W * nc * 64 * ks + (size_t)W * nf * 1024 + (size_t)W * 128 +
+         (size_t)W * 16 * 64 * ks;
+}
+
+bool dq_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 3 || c.split_k != 1 || c.bm != 16) return false;
+  for (auto t : kDq)
+    if (t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
+      return K == (int64_t)64 * t.ks * t.w && dq_lds_bytes(t.nc, t.ks, t.w) <= kMaxLds;
+  return false;
+}
+
+// The untuned choice: 16 waves that take K in one step each, 16 columns a workgroup (8 for
+// narrow N).
+bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
+  const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : 8;
+  for (int ks : {2, 4}) {
+    const i8l_config t{16, nc, 64 * ks, 16, 3, 1, 1};
+    if (K == (int64_t)64 * ks * 16 && dq_ok(t, K)) {
+      *c = t;
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int NC, int KS, int W, int P, int EK, int DT>
+hipError_t launch_dq_k(const uint16_t* x, int64_t ldx, const int8_t* b, int64_t ldb,
+                       const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  auto kern = gemm_wlds1_dq<NC, KS, W, P, EK, DT>;
+  const size_t shm = dq_lds_bytes(NC, KS, W);
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
+  const dim3 grid(e.N / NC, (e.M + 15) / 16);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, x, ldx, b, ldb, e, sa_out, precise);
+  return hipGetLastError();
+}
+
+template <int NC, int KS, int W, int P>
+hipError_t launch_dq_p(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  if (act_dtype == I8L_F16)
+    return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_F16>(x, ldx, b, ldb, e, sa_out, precise, st);
+  switch (epi_kind(e)) {
+    case EK_BF16:
+      return launch_dq_k<NC, KS, W, P, EK_BF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
+                                                          st);
+    case EK_BF16_BBF16:
+      return launch_dq_k<NC, KS, W, P, EK_BF16_BBF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out,
+                                                                precise, st);
+    default:
+      return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
+                                                         st);
+  }
+}
+
+// Passes of the quantizer prologue: ceil(rows / RPP) for the block's valid rows, taken as
+// the next power of two (P in {1, 2, 4, ...}, at most 16 rows).
+template <int NC, int KS, int W>
+hipError_t launch_dq_t(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  constexpr int RPP = 64 / (8 * KS);
+  const int rows = e.M < 16 ? e.M : 16;
+  const int need = (rows + RPP - 1) / RPP;
+  if (need <= 1)
+    return launch_dq_p<NC, KS, W, 1>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if (need <= 2)
+    return launch_dq_p<NC, KS, W, 2>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if constexpr (16 / RPP >= 4)
+    if (need <= 4)
+      return launch_dq_p<NC, KS, W, 4>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  if constexpr (16 / RPP >= 8)
+    if (need <= 8)
+      return launch_dq_p<NC, KS, W, 8>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
+                     const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
+                     hipStream_t st) {
+  const int nc = c.bn, ks = c.bk / 64, W = c.warps;
+#define I8L_DQ(NC_, KS_, W_)                                                                \
+  if (nc == NC_ && ks == KS_ && W == W_)                                                    \
+    return launch_dq_t<NC_, KS_, W_>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+  I8L_DQ(8, 2, 16) I8L_DQ(16, 2, 16) I8L_DQ(32, 2, 16) I8L_DQ(8, 4, 16) I8L_DQ(16, 4, 16)
+#undef I8L_DQ
+  return hipErrorInvalidValue;
+}
+
+}  // namespace i8l

@@ -5,7 +5,7 @@
 The same Python surface as the reference's int8_linear/kernel.py (AshrithaG/int8-linear):
 Config, NotSupported, default_config, tuned_config, choose_config and w8a8_mm, with the
 same argument meaning, validation order and exceptions (kernel.py:45-60, 127-160, 202-242).
-The kernel itself is hand-written HIP in csrc/i8l_gemm.hip, reached through the C ABI of
+The kernel itself is hand-written HIP in csrc/i8l_gemm*.hip, reached through the C ABI of
 include/int8_linear_amd.h: an int8 MFMA (v_mfma_i32_16x16x64_i8 / 32x32x32_i8) product
 accumulated exactly in int32, then acc * scale_a * scale_b + bias in fp32 and one cast.
 
