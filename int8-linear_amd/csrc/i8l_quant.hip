@@ -89,12 +89,14 @@ struct RowPos {
   int lane;
 };
 
+// MULTI false: one wave a row (nw == 1), so no division.
+template <bool MULTI>
 __device__ __forceinline__ RowPos row_pos(int nw, int rpb) {
   RowPos p;
   const int wave = threadIdx.x >> 6;
   p.lane = threadIdx.x & 63;
-  p.rw = wave % nw;
-  p.slot = wave / nw;
+  p.rw = MULTI ? wave % nw : 0;
+  p.slot = MULTI ? wave / nw : wave;
   p.row = (int64_t)blockIdx.x * rpb + p.slot;
   return p;
 }
@@ -115,11 +117,12 @@ __device__ __forceinline__ void unpack8(uint4 v, float* o) {
 }
 
 // Elements [e0, e0+8) of a row of length n as floats (zeros past the end).  VEC: n is a
-// multiple of 8 and the row is 16-byte aligned, so a chunk is all in or all out.
-template <int DT, bool VEC>
+// multiple of 8 and the row is 16-byte aligned, so a chunk is all in or all out.  FULL (with
+// VEC): the row fills the launch's chunks exactly, so every chunk is in and nothing is checked.
+template <int DT, bool VEC, bool FULL = false>
 __device__ __forceinline__ void load8(const uint16_t* p, int e0, int n, float* o) {
   if (VEC) {
-    if (e0 < n) {
+    if (FULL || e0 < n) {
       unpack8<DT>(*(const uint4*)(p + e0), o);
     } else {
 #pragma unroll
@@ -132,9 +135,9 @@ __device__ __forceinline__ void load8(const uint16_t* p, int e0, int n, float* o
 }
 
 // The 16-bit elements [e0, e0+8) of a row packed as they lie in memory (zeros past the end).
-template <bool VEC>
+template <bool VEC, bool FULL = false>
 __device__ __forceinline__ uint4 load_raw8(const uint16_t* p, int e0, int n) {
-  if (VEC) return e0 < n ? *(const uint4*)(p + e0) : make_uint4(0, 0, 0, 0);
+  if (VEC) return FULL || e0 < n ? *(const uint4*)(p + e0) : make_uint4(0, 0, 0, 0);
   uint32_t w[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -157,10 +160,10 @@ __device__ __forceinline__ void unpack_pair(const uint4& v, int i, float& a, flo
   }
 }
 
-template <int DT, bool VEC>
+template <int DT, bool VEC, bool FULL = false>
 __device__ __forceinline__ void store8(uint16_t* p, int e0, int n, const float* v) {
   if (VEC) {
-    if (e0 < n) {
+    if (FULL || e0 < n) {
       uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = f32x2_to_act2<DT>(v[2 * i], v[2 * i + 1]);
@@ -187,7 +190,7 @@ __device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float
 
 // The quantizer of a row whose values y (J chunks of 8 per lane) are final: absmax over the
 // row, scale and reciprocal, codes stored as 8-byte pieces, the scale by the row's first lane.
-template <int J, bool VEC, bool MULTI>
+template <int J, bool VEC, bool MULTI, bool FULL = false>
 __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p, int n, int nw,
                                                int8_t* qrow, float* scale_out, int precise,
                                                float* sh) {
@@ -216,7 +219,7 @@ __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p
       c[i] = (uint32_t)(int)v & 0xffu;
     }
     if (VEC) {
-      if (e0 < n) {
+      if (FULL || e0 < n) {
         const uint32_t lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
         const uint32_t hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
         *(uint2*)(qrow + e0) = make_uint2(lo, hi);
@@ -230,42 +233,22 @@ __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p
 }
 
 // ------------------------------------------------------------------ add + RMSNorm + quant
-// J and NW are powers of two, so each wave covers an aligned power-of-two span of the row
-// and the wave/chunk/lane reductions together evaluate the padded row's pairwise tree.
-template <int J, int DT, int WDT, bool VEC, bool RES, bool MULTI>
-__global__ void __launch_bounds__(1024)
-add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
-                         const uint16_t* __restrict__ w, float eps, int8_t* __restrict__ q,
-                         float* __restrict__ scale, uint16_t* __restrict__ rout, int64_t M,
-                         int H, int nw, int rpb, int precise) {
-  __shared__ double dsh[kMaxWaves];
-  __shared__ float fsh[kMaxWaves];
-  const RowPos p = row_pos(nw, rpb);
-  if (p.row >= M) return;  // whole single-wave rows only: a row of nw > 1 waves has rpb = 1
-  const int64_t ro = p.row * H;
-  float xv[J][8];
-#pragma unroll
-  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + ro, chunk_base<J>(p, j), H, xv[j]);
-  if constexpr (RES) {
-    float rv[J][8];
-#pragma unroll
-    for (int j = 0; j < J; ++j) load8<DT, VEC>(res + ro, chunk_base<J>(p, j), H, rv[j]);
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xv[j][i] = xv[j][i] + rv[j][i];
-      store8<DT, VEC>(rout + ro, chunk_base<J>(p, j), H, xv[j]);
-    }
-  }
-  // sum of squares: leaves in-lane, then lanes, then the wave's chunks, then waves
+// The sum of squares of a wave's J chunks: leaves in-lane, then lanes, then the chunks.
+// x_i^2 is exact in double (24-bit significands), so the first level's x_i^2 + x_{i+1}^2 is
+// one fma: RN(x_{i+1}^2 + s) equals RN(RN(x_{i+1}^2) + s) when x_{i+1}^2 is exact.
+template <int J>
+__device__ __forceinline__ double wave_sumsq(const float (&xv)[J][8]) {
   double node[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     double s[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = (double)xv[j][i] * (double)xv[j][i];
+    for (int i = 0; i < 8; i += 2) {
+      const double a = (double)xv[j][i], b = (double)xv[j][i + 1];
+      s[i] = __builtin_fma(b, b, a * a);
+    }
 #pragma unroll
-    for (int st = 1; st < 8; st <<= 1)
+    for (int st = 2; st < 8; st <<= 1)
 #pragma unroll
       for (int i = 0; i < 8; i += 2 * st) s[i] = s[i] + s[i + st];
     node[j] = wave_tree_sum(s[0]);
@@ -274,7 +257,81 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
   for (int st = 1; st < J; st <<= 1)
 #pragma unroll
     for (int j = 0; j < J; j += 2 * st) node[j] = node[j] + node[j + st];
-  double tot = node[0];
+  return node[0];
+}
+
+// y = cast_x( f32(cast_w(x * rs)) * f32(w) ) for the 8 elements of a chunk.
+template <int DT, int WDT>
+__device__ __forceinline__ void norm_chunk(float (&xv)[8], float rs, const float (&wv)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float a = xv[i] * rs, b = xv[i + 1] * rs;
+    round_through2<WDT>(a, b);
+    a = a * wv[i];
+    b = b * wv[i + 1];
+    round_through2<DT>(a, b);
+    xv[i] = a;
+    xv[i + 1] = b;
+  }
+}
+
+// J and NW are powers of two, so each wave covers an aligned power-of-two span of the row
+// and the wave/chunk/lane reductions together evaluate the padded row's pairwise tree.
+// FULL (row length exactly NW*J*512): no bounds checks, and every load of the row and of the
+// weight vector is issued up front, before any arithmetic (the scheduler would otherwise sink
+// the weight loads behind the reduction, where their latency is exposed).
+template <int J, int DT, int WDT, bool VEC, bool RES, bool MULTI, bool FULL>
+__global__ void __launch_bounds__(1024)
+add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+                         const uint16_t* __restrict__ w, float eps, int8_t* __restrict__ q,
+                         float* __restrict__ scale, uint16_t* __restrict__ rout, int64_t M,
+                         int H, int nw, int rpb, int precise) {
+  static_assert(!FULL || VEC, "FULL rows are vector rows");
+  __shared__ double dsh[kMaxWaves];
+  __shared__ float fsh[kMaxWaves];
+  const RowPos p = row_pos<MULTI>(nw, rpb);
+  if (p.row >= M) return;  // whole single-wave rows only: a row of nw > 1 waves has rpb = 1
+  const int64_t ro = p.row * H;
+  float xv[J][8];
+  uint4 wr[J];
+  if constexpr (FULL) {
+    uint4 xr[J], rr[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      xr[j] = *(const uint4*)(x + ro + chunk_base<J>(p, j));
+      if constexpr (RES) rr[j] = *(const uint4*)(res + ro + chunk_base<J>(p, j));
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) wr[j] = *(const uint4*)(w + chunk_base<J>(p, j));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      unpack8<DT>(xr[j], xv[j]);
+      if constexpr (RES) {
+        float rv[8];
+        unpack8<DT>(rr[j], rv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[j][i] = xv[j][i] + rv[i];
+        store8<DT, true, true>(rout + ro, chunk_base<J>(p, j), H, xv[j]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; ++j) load8<DT, VEC>(x + ro, chunk_base<J>(p, j), H, xv[j]);
+    if constexpr (RES) {
+      float rv[J][8];
+#pragma unroll
+      for (int j = 0; j < J; ++j) load8<DT, VEC>(res + ro, chunk_base<J>(p, j), H, rv[j]);
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[j][i] = xv[j][i] + rv[j][i];
+        store8<DT, VEC>(rout + ro, chunk_base<J>(p, j), H, xv[j]);
+      }
+    }
+  }
+  // sum of squares: the wave's node, then the waves of the row
+  double tot = wave_sumsq<J>(xv);
   if constexpr (MULTI) {
     // the nw wave nodes (aligned, a power of two of them) become lanes 0..nw-1 of a tree
     // whose other leaves are +0, which leaves every sum unchanged
@@ -287,37 +344,33 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     float wv[8];
-    load8<WDT, VEC>(w, chunk_base<J>(p, j), H, wv);
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float a = xv[j][i] * rs, b = xv[j][i + 1] * rs;
-      round_through2<WDT>(a, b);
-      a = a * wv[i];
-      b = b * wv[i + 1];
-      round_through2<DT>(a, b);
-      xv[j][i] = a;
-      xv[j][i + 1] = b;
-    }
+    if constexpr (FULL)
+      unpack8<WDT>(wr[j], wv);
+    else
+      load8<WDT, VEC>(w, chunk_base<J>(p, j), H, wv);
+    norm_chunk<DT, WDT>(xv[j], rs, wv);
   }
-  quantize_store<J, VEC, MULTI>(xv, p, H, nw, q + ro, scale + p.row, precise, fsh);
+  quantize_store<J, VEC, MULTI, FULL>(xv, p, H, nw, q + ro, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ SiLU-and-mul + quant
-template <int J, int DT, bool VEC, bool ROUND, bool MULTI>
+// FULL (row length exactly NW*J*512): no bounds checks.
+template <int J, int DT, bool VEC, bool ROUND, bool MULTI, bool FULL>
 __global__ void __launch_bounds__(1024)
 silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
                       float* __restrict__ scale, int64_t M, int I, int nw, int rpb,
                       int precise) {
   __shared__ float fsh[kMaxWaves];
-  const RowPos p = row_pos(nw, rpb);
+  const RowPos p = row_pos<MULTI>(nw, rpb);
   if (p.row >= M) return;
   const uint16_t* grow = gu + p.row * 2 * I;
   uint4 graw[J], uraw[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    graw[j] = load_raw8<VEC>(grow, chunk_base<J>(p, j), I);
-    uraw[j] = load_raw8<VEC>(grow + I, chunk_base<J>(p, j), I);
+    graw[j] = load_raw8<VEC, FULL>(grow, chunk_base<J>(p, j), I);
+    uraw[j] = load_raw8<VEC, FULL>(grow + I, chunk_base<J>(p, j), I);
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load of the row in flight before the arithmetic
   // d = 1 + exp(-g).  The range selects of canon_expf do not change d: below the normal
   // range exp is < 2^-24 and 1 + e rounds to 1 either way, the clamp already overflows
   // to +inf above 89, and a NaN g makes the quotient NaN whatever d is (checked for every
@@ -374,21 +427,21 @@ silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
         y[j][2 * i + 1] = a[1];
       }
   }
-  quantize_store<J, VEC, MULTI>(y, p, I, nw, q + p.row * I, scale + p.row, precise, fsh);
+  quantize_store<J, VEC, MULTI, FULL>(y, p, I, nw, q + p.row * I, scale + p.row, precise, fsh);
 }
 
 // ------------------------------------------------------------------ plain per-token quant
-template <int J, int DT, bool VEC, bool MULTI>
+template <int J, int DT, bool VEC, bool MULTI, bool FULL>
 __global__ void __launch_bounds__(1024)
 quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
              float* __restrict__ scale, int64_t M, int H, int nw, int rpb, int precise) {
   __shared__ float fsh[kMaxWaves];
-  const RowPos p = row_pos(nw, rpb);
+  const RowPos p = row_pos<MULTI>(nw, rpb);
   if (p.row >= M) return;
   float y[J][8];
 #pragma unroll
-  for (int j = 0; j < J; ++j) load8<DT, VEC>(x + p.row * ldx, chunk_base<J>(p, j), H, y[j]);
-  quantize_store<J, VEC, MULTI>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
+  for (int j = 0; j < J; ++j) load8<DT, VEC, FULL>(x + p.row * ldx, chunk_base<J>(p, j), H, y[j]);
+  quantize_store<J, VEC, MULTI, FULL>(y, p, H, nw, q + p.row * H, scale + p.row, precise, fsh);
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -411,7 +464,8 @@ struct Geom {
 // Up to this many waves in total, a row is spread over as many waves as possible (one chunk
 // a lane): a few rows are latency-bound, and more waves shorten each lane's serial work.
 // Beyond it, each wave takes up to 4 chunks a lane, which keeps more bytes in flight per
-// wave and reduces cross-wave reductions.
+// wave and reduces cross-wave reductions.  The RMSNorm spreads only up to half as many
+// waves: from 1024 rows of 2048 a wave a row (no cross-wave reduction) is the faster.
 constexpr int64_t kSpreadWaves = 4096;
 
 // RMSNorm: powers of two throughout (the sum tree needs aligned power-of-two spans).
@@ -419,7 +473,7 @@ Geom norm_geom(int64_t M, int h, bool vec) {
   const int p = next_pow2(h);
   Geom g;
   const int64_t spread = (int64_t)M * ((p + 511) / 512);
-  if (vec && spread <= kSpreadWaves) {
+  if (vec && spread <= kSpreadWaves / 2) {
     g.nw = p / 512 < 1 ? 1 : p / 512;
     g.j = 1;
     while (g.nw > kMaxWaves) g.nw /= 2, g.j *= 2;
@@ -447,6 +501,26 @@ Geom flat_geom(int64_t M, int n, bool vec) {
   return g;
 }
 
+// SiLU-and-mul: many operations an element, so rows stay spread over more waves than in the
+// max-only kernels: one chunk a lane while the launch has at most kSiluWaves waves, two
+// chunks up to twice that, then the max-only kernels' geometry (up to four chunks a lane).
+constexpr int64_t kSiluWaves = 8192;
+Geom silu_geom(int64_t M, int n, bool vec) {
+  const int chunks = (n + 7) / 8;
+  if (vec)
+    for (int j = 1; j <= 2; j *= 2) {
+      const int nw = (chunks + 64 * j - 1) / (64 * j);
+      if (nw <= kMaxWaves && (int64_t)M * nw <= kSiluWaves * j) {
+        Geom g;
+        g.j = j;
+        g.nw = nw;
+        g.rpb = nw == 1 ? 4 : 1;
+        return g;
+      }
+    }
+  return flat_geom(M, n, vec);
+}
+
 dim3 grid_of(int64_t M, const Geom& g) { return dim3((unsigned)((M + g.rpb - 1) / g.rpb)); }
 dim3 block_of(const Geom& g) { return dim3(64 * g.nw * g.rpb); }
 
@@ -456,13 +530,18 @@ template <int DT, int WDT, bool RES, bool MULTI>
 void launch_norm_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
                    const uint16_t* res, const uint16_t* w, float eps, int8_t* q, float* scale,
                    uint16_t* rout, int64_t M, int H, int precise) {
-#define I8L_NORM(J_, V_)                                                                    \
-  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<J_, DT, WDT, V_, RES, MULTI>), grid, block_of(g), \
-                     0, st, x, res, w, eps, q, scale, rout, M, H, g.nw, g.rpb, precise)
-  if (!vec) I8L_NORM(4, false);
-  else if (g.j == 1) I8L_NORM(1, true);
-  else if (g.j == 2) I8L_NORM(2, true);
-  else I8L_NORM(4, true);
+#define I8L_NORM(J_, V_, F_)                                                                \
+  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<J_, DT, WDT, V_, RES, MULTI, F_>), grid,      \
+                     block_of(g), 0, st, x, res, w, eps, q, scale, rout, M, H, g.nw, g.rpb,   \
+                     precise)
+  const bool full = vec && H == 512 * g.j * g.nw;
+  if (!vec) I8L_NORM(4, false, false);
+  else if (g.j == 1 && full) I8L_NORM(1, true, true);
+  else if (g.j == 1) I8L_NORM(1, true, false);
+  else if (g.j == 2 && full) I8L_NORM(2, true, true);
+  else if (g.j == 2) I8L_NORM(2, true, false);
+  else if (full) I8L_NORM(4, true, true);
+  else I8L_NORM(4, true, false);
 #undef I8L_NORM
 }
 
@@ -482,14 +561,18 @@ void launch_norm(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint1
 template <int DT, bool ROUND, bool MULTI>
 void launch_silu_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* gu,
                    int8_t* q, float* scale, int64_t M, int I, int precise) {
-#define I8L_SILU(J_, V_)                                                                    \
-  hipLaunchKernelGGL((silu_mul_quant_kernel<J_, DT, V_, ROUND, MULTI>), grid, block_of(g), 0, \
-                     st, gu, q, scale, M, I, g.nw, g.rpb, precise)
-  if (!vec) I8L_SILU(4, false);
-  else if (g.j == 1) I8L_SILU(1, true);
-  else if (g.j == 2) I8L_SILU(2, true);
-  else if (g.j == 3) I8L_SILU(3, true);
-  else I8L_SILU(4, true);
+#define I8L_SILU(J_, V_, F_)                                                                \
+  hipLaunchKernelGGL((silu_mul_quant_kernel<J_, DT, V_, ROUND, MULTI, F_>), grid, block_of(g), \
+                     0, st, gu, q, scale, M, I, g.nw, g.rpb, precise)
+  const bool full = vec && I == 512 * g.j * g.nw;
+  if (!vec) I8L_SILU(4, false, false);
+  else if (g.j == 1 && full) I8L_SILU(1, true, true);
+  else if (g.j == 1) I8L_SILU(1, true, false);
+  else if (g.j == 2 && full) I8L_SILU(2, true, true);
+  else if (g.j == 2) I8L_SILU(2, true, false);
+  else if (g.j == 3) I8L_SILU(3, true, false);
+  else if (full) I8L_SILU(4, true, true);
+  else I8L_SILU(4, true, false);
 #undef I8L_SILU
 }
 
@@ -505,14 +588,16 @@ void launch_silu(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint1
 template <int DT, bool MULTI>
 void launch_quant_k(const Geom& g, bool vec, dim3 grid, hipStream_t st, const uint16_t* x,
                     int64_t ldx, int8_t* q, float* scale, int64_t M, int H, int precise) {
-#define I8L_QUANT(J_, V_)                                                                   \
-  hipLaunchKernelGGL((quant_kernel<J_, DT, V_, MULTI>), grid, block_of(g), 0, st, x, ldx, q, \
-                     scale, M, H, g.nw, g.rpb, precise)
-  if (!vec) I8L_QUANT(4, false);
-  else if (g.j == 1) I8L_QUANT(1, true);
-  else if (g.j == 2) I8L_QUANT(2, true);
-  else if (g.j == 3) I8L_QUANT(3, true);
-  else I8L_QUANT(4, true);
+#define I8L_QUANT(J_, V_, F_)                                                               \
+  hipLaunchKernelGGL((quant_kernel<J_, DT, V_, MULTI, F_>), grid, block_of(g), 0, st, x, ldx, \
+                     q, scale, M, H, g.nw, g.rpb, precise)
+  const bool full = vec && H == 512 * g.j * g.nw;
+  if (!vec) I8L_QUANT(4, false, false);
+  else if (g.j == 1) I8L_QUANT(1, true, false);
+  else if (g.j == 2) I8L_QUANT(2, true, false);
+  else if (g.j == 3) I8L_QUANT(3, true, false);
+  else if (full) I8L_QUANT(4, true, true);
+  else I8L_QUANT(4, true, false);
 #undef I8L_QUANT
 }
 
@@ -585,7 +670,7 @@ extern "C" int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale, 
   if (M == 0) return I8L_OK;
   const int i = (int)I;
   const bool vec = i % 8 == 0 && a16(gate_up) && a16(q);
-  const Geom g = flat_geom(M, i, vec);
+  const Geom g = silu_geom(M, i, vec);
   const hipStream_t st = (hipStream_t)stream;
   auto go = [&](auto launch) {
     launch(g, vec, grid_of(M, g), st, (const uint16_t*)gate_up, q, scale, M, i, precise_div);

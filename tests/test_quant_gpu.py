@@ -77,10 +77,11 @@ def check_norm(x, r, w, precise=True):
 
 # Beyond the reference's shapes, rows that exercise every launch geometry of the kernel:
 # one chunk a lane (100), two (520, 1001 unaligned), rows of 2, 4, 8 and 16 waves
-# (4096, 6144, 16384, 32768), and M not a multiple of the 4 rows a workgroup holds.
+# (4096, 6144, 16384, 32768), M not a multiple of the 4 rows a workgroup holds, and rows
+# that fill their waves exactly with one wave a row (1030 x 2048) or two (300 x 4096).
 @pytest.mark.parametrize("m,k", [(1, 2048), (7, 2048), (64, 1024), (300, 2048), (5, 1000),
                                  (3, 13), (2, 6144), (6, 100), (9, 520), (5, 1001), (5, 4096),
-                                 (2, 16384), (3, 32768)])
+                                 (2, 16384), (3, 32768), (1030, 2048), (300, 4096)])
 @pytest.mark.parametrize("has_res", [False, True])
 def test_add_rmsnorm_quant(m, k, has_res):
     say(f"add_rmsnorm_quant m={m} k={k} res={has_res}")
@@ -132,12 +133,12 @@ def test_silu_mul_quant(m, i, round_silu):
     assert_close_int8(q, s, *ref_silu(gu, round_silu))
 
 
-@pytest.mark.parametrize("i", [64, 6144])
-def test_silu_mul_quant_extreme_gates(i):
+@pytest.mark.parametrize("i,m", [(64, 6), (6144, 6), (6144, 1100), (6144, 2800)])
+def test_silu_mul_quant_extreme_gates(i, m):
     """Gates of -0.0 and at or below -87 (where 1 + exp(-g) is huge or infinite) send their
-    wave to the IEEE-division path; the other rows of the same launch stay on the fast path."""
-    say(f"silu_mul_quant extreme gates i={i}")
-    m = 6
+    wave to the IEEE-division path; the other rows of the same launch stay on the fast path.
+    The three 6144-wide cases take one, two and four chunks a lane."""
+    say(f"silu_mul_quant extreme gates i={i} m={m}")
     gu = randn((m, 2 * i), 80 + i, 2.0).cpu()
     special = torch.tensor([-0.0, -87.0, -87.5, -88.0, -89.0, -100.0, -1e30, -3e38, 0.0, 87.5],
                            dtype=torch.bfloat16)
