@@ -67,6 +67,17 @@ def silu_bytes(m: int, i: int) -> int:
     return 5 * m * i + 4 * m
 
 
+def warm_up(g, seconds: float = 0.03) -> None:
+    """Replays a graph for `seconds` before it is timed.  After the GPU has idled (operand
+    set-up on the host), sustained matrix work runs up to ~15% slower for the first ~20 ms
+    while the clocks settle; the timed windows then see the steady state."""
+    import torch
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        g.replay()
+        torch.cuda.synchronize()
+
+
 def graph_time_us(fn, calls: int, windows: int = 5) -> float:
     """Median microseconds per call of `calls` back-to-back calls captured in one graph."""
     import torch
@@ -82,6 +93,7 @@ def graph_time_us(fn, calls: int, windows: int = 5) -> float:
             fn(i)
     g.replay()
     torch.cuda.synchronize()
+    warm_up(g)
     out = []
     for _ in range(windows):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

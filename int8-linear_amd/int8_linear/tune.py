@@ -24,6 +24,7 @@ import argparse
 import json
 import statistics
 import sys
+import time
 from dataclasses import asdict
 
 import torch
@@ -52,7 +53,9 @@ DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
               (256, 128, 64, 8, 4), (128, 256, 64, 8, 4), (128, 256, 128, 8, 3),
               (256, 128, 128, 8, 3), (128, 128, 64, 4, 4), (128, 128, 128, 4, 4),
               (64, 128, 128, 4, 4), (64, 256, 128, 8, 3), (64, 128, 64, 4, 6),
-              (64, 128, 128, 4, 6), (64, 64, 128, 4, 4), (128, 64, 128, 4, 4)]
+              (64, 128, 128, 4, 6), (64, 64, 128, 4, 4), (128, 64, 128, 4, 4),
+              (128, 384, 64, 8, 3), (128, 384, 64, 8, 4), (128, 192, 64, 4, 4),
+              (256, 192, 64, 4, 4)]
 
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
@@ -110,6 +113,10 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
     return out
 
 
+FINALISTS = 4      # candidates timed again, in turn, before one is chosen
+FINAL_ROUNDS = 2   # extra timings of each finalist
+
+
 def time_cold_us(call, copies: int, windows: int = 3) -> float:
     """Median us per call of 2*copies back-to-back calls in one HIP graph."""
     side = torch.cuda.Stream()
@@ -125,6 +132,13 @@ def time_cold_us(call, copies: int, windows: int = 3) -> float:
             call(i)
     g.replay()
     torch.cuda.synchronize()
+    # After the GPU has idled, sustained matrix work runs up to ~15% slower for the first
+    # ~20 ms while the clocks settle: replay for 30 ms first, so every candidate is timed in
+    # the steady state rather than the first ones at a disadvantage.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.03:
+        g.replay()
+        torch.cuda.synchronize()
     res = []
     for _ in range(windows):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -149,8 +163,8 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print) -> dict:
         a_q, a_s = a["a_q"], a["a_s"]
         one = torch.ones(1, device=device)
         ref = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=default_config(m, n, k))
-        best = None
         t0 = None
+        timed = []
         for cfg in candidate_configs(m, k, n):
             got = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=cfg)
             if not torch.equal(got, ref):
@@ -159,8 +173,18 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print) -> dict:
                                                        torch.bfloat16, config=c), copies)
             if cfg == default_config(m, n, k):
                 t0 = us
-            if best is None or us < best[1]:
-                best = (cfg, us)
+            timed.append((us, cfg))
+        # One pass ranks candidates only to within a few percent (clock and cache state drift
+        # over the sweep): the FINALISTS fastest are timed again, in turn, and the best median
+        # of their timings wins.
+        timed.sort(key=lambda t: t[0])
+        finals = {c: [us] for us, c in timed[:FINALISTS]}
+        for _ in range(FINAL_ROUNDS):
+            for c in finals:
+                finals[c].append(time_cold_us(lambda i, c=c: w8a8_mm(
+                    a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16, config=c), copies))
+        best = min(((statistics.median(v), c) for c, v in finals.items()), key=lambda t: t[0])
+        best = (best[1], best[0])
         if t0 is None:
             t0 = time_cold_us(lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16,
                                                 config=default_config(m, n, k)), copies)
@@ -187,6 +211,8 @@ def main() -> int:
     ap.add_argument("--shapes", default="qwen3-1.7b-vllm")
     ap.add_argument("--m", default="1,2,4,8,16,17,32,64,128",
                     help="comma-separated M values, or capture (vLLM graph batch sizes)")
+    ap.add_argument("--kn", default=None,
+                    help="comma-separated KxN shapes of the preset to tune (default: all)")
     ap.add_argument("--merge", action="store_true", help="write the result into tuned_configs.json")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
@@ -194,7 +220,10 @@ def main() -> int:
     arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
     ms = parse_ms(args.m)
     table = {}
+    only = set(args.kn.split(",")) if args.kn else None
     for label, k, n in SHAPES[args.shapes]:
+        if only is not None and f"{k}x{n}" not in only:
+            continue
         table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True))
     if args.out:
         with open(args.out, "w") as f:

@@ -62,6 +62,23 @@ def test_default_config_regimes():
         assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
 
 
+def test_every_tuner_candidate_tile_is_built():
+    """The tuner's tile lists and the library's built tiles stay in step: each listed tile
+    is taken for a shape it divides."""
+    from int8_linear import tune
+    n, k = 2 * 3 * 128 * 8, 4096                            # divisible by every tile width
+    for bm, bn, bk, w, st in tune.DMAP_TILES:
+        assert kernel.supported(1024, n, k, Config(bm, bn, bk, w, st + tune.PIPELINED, 4)), bn
+    for bm, bn, bk, w, st in tune.DMA_TILES:
+        assert kernel.supported(1024, n, k, Config(bm, bn, bk, w, st, 1)), (bm, bn, bk, st)
+    for bm, bn, bk, w in tune.STAGED_TILES:
+        assert kernel.supported(1024, n, k, Config(bm, bn, bk, w, 2, 1)), (bm, bn, bk)
+    for mt, nc, ks in tune.WLDS_TILES:                     # one or more K steps a wave
+        assert any(kernel.supported(16 * mt, n, steps * w * 64 * ks,
+                                    Config(16 * mt, nc, 64 * ks, w, 3, 1))
+                   for w in (4, 8, 16) for steps in (1, 2)), (mt, nc, ks)
+
+
 def test_supported_decline_rule_matches_reference():
     # kernel.py:228-229 of the reference: N % bn or K % bk declines
     assert not kernel.supported(4, 64, 100)

@@ -94,6 +94,28 @@ def test_exact_under_other_tilings(config, m):
     assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
 
 
+# Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
+# 12288), exact on N = 1536 with ragged M.
+WIDE_TILINGS = [Config(128, 384, 64, 8, 11, 4), Config(128, 384, 64, 8, 12, 8),
+                Config(128, 192, 64, 4, 12, 8), Config(256, 192, 64, 4, 12, 4)]
+
+
+@pytest.mark.parametrize("config", WIDE_TILINGS, ids=lambda c: c.name.replace(" ", "_"))
+@pytest.mark.parametrize("m", [256, 300])
+def test_exact_under_wide_tilings(config, m):
+    k, n = 2048, 1536
+    say(f"w8a8_mm wide m={m} k={k} n={n} config={config.name}")
+    a, w = ints((m, k), 5), ints((n, k), 6)
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, w.t(), one, one, raw=True, config=config)
+    assert np.array_equal(np_(got), o.gemm_i32(np_(a), np_(w)))
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    bias = (torch.randn(n, device="cuda") * 0.01).to(torch.bfloat16)
+    out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, bias, config=config)
+    assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, bias, torch.bfloat16))
+
+
 # The weights-through-LDS decode schedule (stages 3, bm <= 128): every built tile, with one,
 # two, three and four K steps a wave (the ring's even and odd tails), 32/16/8/4 columns a
 # workgroup, ragged M.
