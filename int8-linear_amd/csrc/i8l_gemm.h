@@ -198,8 +198,11 @@ __host__ __device__ constexpr bool wlds_multi_fits(int mt, int nc, int ks) {
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per CU, bytes
 constexpr int kPipelined = 8;           // the overlapped-ring configs' stages: ring depth + 8
 
-// Workgroup barrier without a memory fence: LDS accesses are ordered around it by the
-// compiler-level fences; waits for outstanding memory are issued explicitly where needed.
+// Workgroup barrier without a memory fence or wait: the compiler keeps LDS accesses on their
+// side of it, but outstanding LDS stores and reads are not waited for (gfx950's s_barrier does
+// not wait, and the compiler adds no wait before it).  It suits the ring turns, where the
+// buffers are written by direct-to-LDS loads that each wave waits for (vmcnt) before the
+// barrier; LDS stores that other waves read after a barrier need __syncthreads().
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();

@@ -73,7 +73,9 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
       }
     }
   }
-  lds_barrier();
+  // Other waves read these stores: the barrier must also wait for them to complete
+  // (s_barrier alone does not, and with two workgroups a CU sharing the LDS they do lag).
+  __syncthreads();
   constexpr int CPR = BN / 8;                  // 16-byte chunks per output row
   static_assert((BM * CPR) % T == 0, "tile rows do not split over the threads");
 #pragma unroll

@@ -94,6 +94,26 @@ def test_exact_under_other_tilings(config, m):
     assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
 
 
+# Regression test for a race in the prefill epilogue: its LDS staging stores were handed to the
+# other waves by a barrier that did not wait for them, and with two workgroups a CU sharing the
+# LDS about one call in ten returned 16x16 blocks of stale LDS bytes (M=700, K=N=2048, 64x64
+# tiles).  Every repeated call must give the oracle's bits.
+@pytest.mark.parametrize("config", [Config(64, 64, 128, 4, 12, 4), Config(128, 64, 128, 4, 12, 4),
+                                    Config(128, 128, 64, 4, 2, 8), Config(128, 128, 64, 4, 4, 1)],
+                         ids=lambda c: c.name.replace(" ", "_"))
+def test_prefill_epilogue_is_repeatable(config):
+    m, k, n = 700, 2048, 2048
+    say(f"w8a8_mm repeated m={m} k={k} n={n} config={config.name}")
+    a, w = ints((m, k), 11), ints((n, k), 12)
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    first = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config)
+    assert np.array_equal(bits(first), oracle_out(a, w, sa, sb, None, torch.bfloat16))
+    outs = [w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config) for _ in range(100)]
+    torch.cuda.synchronize()
+    assert sum(not torch.equal(o, first) for o in outs) == 0
+
+
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
 # 12288), exact on N = 1536 with ragged M.
 WIDE_TILINGS = [Config(128, 384, 64, 8, 11, 4), Config(128, 384, 64, 8, 12, 8),
