@@ -114,6 +114,33 @@ def test_prefill_epilogue_is_repeatable(config):
     assert sum(not torch.equal(o, first) for o in outs) == 0
 
 
+def _prefill_tiles():
+    from int8_linear import tune
+    out = [Config(bm, bn, bk, w, st + tune.PIPELINED, 4) for bm, bn, bk, w, st in tune.DMAP_TILES]
+    out += [Config(bm, bn, bk, w, st, 1) for bm, bn, bk, w, st in tune.DMA_TILES]
+    out += [Config(bm, bn, bk, w, 2, 1) for bm, bn, bk, w in tune.STAGED_TILES]
+    return out
+
+
+@pytest.mark.parametrize("m,n", [(700, 2304), (300, 4608)])
+def test_every_prefill_tile_is_repeatable(m, n):
+    """Every prefill tile the tuner may pick, called 20 times in a row at a shape where two
+    workgroups share a CU, gives the same bits each time and the oracle's bits."""
+    k = 2048
+    say(f"w8a8_mm every prefill tile repeated m={m} k={k} n={n}")
+    a, w = ints((m, k), 13), ints((n, k), 14)
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    want = oracle_out(a, w, sa, sb, None, torch.bfloat16)
+    for config in _prefill_tiles():
+        if not kernel.supported(m, n, k, config):
+            continue
+        outs = [w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config) for _ in range(20)]
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(outs[0]), want), config.name
+        assert all(torch.equal(o, outs[0]) for o in outs), config.name
+
+
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
 # 12288), exact on N = 1536 with ragged M.
 WIDE_TILINGS = [Config(128, 384, 64, 8, 11, 4), Config(128, 384, 64, 8, 12, 8),
