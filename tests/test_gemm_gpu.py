@@ -141,6 +141,33 @@ def test_every_prefill_tile_is_repeatable(m, n):
         assert all(torch.equal(o, outs[0]) for o in outs), config.name
 
 
+@pytest.mark.parametrize("m", [16, 100])
+def test_every_decode_tile_is_repeatable(m):
+    """Every decode tile the tuner may pick (weights through LDS or streamed), called 10 times
+    in a row, gives the same bits each time and the oracle's bits."""
+    from int8_linear import tune
+    k, n = 2048, 4096
+    say(f"w8a8_mm every decode tile repeated m={m} k={k} n={n}")
+    a, w = ints((m, k), 15), ints((n, k), 16)
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    want = oracle_out(a, w, sa, sb, None, torch.bfloat16)
+    configs = [Config(16 * mt, nc, 64 * ks, w_, 3, 1) for mt, nc, ks in tune.WLDS_TILES
+               for w_ in (4, 8, 16)]
+    configs += [Config(16 * mt, bn, 64 * w_, w_, 1, 1) for mt, bn in tune.STREAM_TILES
+                for w_ in (1, 2, 4, 8, 16)]
+    checked = 0
+    for config in configs:
+        if not kernel.supported(m, n, k, config):
+            continue
+        outs = [w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config) for _ in range(10)]
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(outs[0]), want), config.name
+        assert all(torch.equal(o, outs[0]) for o in outs), config.name
+        checked += 1
+    assert checked >= 40
+
+
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
 # 12288), exact on N = 1536 with ragged M.
 WIDE_TILINGS = [Config(128, 384, 64, 8, 11, 4), Config(128, 384, 64, 8, 12, 8),
