@@ -191,8 +191,10 @@ def schedule_of(cfg, k: int) -> str:
         return "gemm_stream"
     if cfg.stages == 2:
         return "gemm_staged"
-    if cfg.stages == 3 and cfg.bm <= 32:
+    if cfg.stages == 3 and cfg.bn <= 32:
         return "gemm_wlds1" if k == cfg.bk * cfg.warps else "gemm_wlds"
+    if cfg.stages == 4 and cfg.bn <= 32:
+        return "gemm_wlds1p"
     return "gemm_dmap" if cfg.stages >= 11 else "gemm_dma"
 
 

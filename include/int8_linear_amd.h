@@ -47,9 +47,12 @@ enum {
  *   bm, bn, bk : output rows (tokens) x output columns x K bytes per workgroup step
  *   warps      : wavefronts (64 lanes) per workgroup
  *   stages     : the schedule: 1 weights streamed into registers (decode); 3 with bm <= 128
- *                and bn <= 32 weights through LDS (decode); 2 LDS staged through registers,
- *                3..8 a ring of that many direct-to-LDS buffers, >= 11 the same ring of
- *                stages - 8 buffers with fragment reads overlapped with the MFMAs (prefill)
+ *                and bn <= 32 weights through LDS (decode); 4 with bn <= 32 the same in one
+ *                K step a wave, each workgroup walking several column tiles with the
+ *                activations held in registers (decode, K == bk * warps); 2 LDS staged
+ *                through registers, 3..8 a ring of that many direct-to-LDS buffers, >= 11 the
+ *                same ring of stages - 8 buffers with fragment reads overlapped with the
+ *                MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order)
  *   split_k    : reserved; must be 1
  * A config the library was not built for returns I8L_UNSUPPORTED.

@@ -239,6 +239,9 @@ hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, cons
                          int64_t ldb, const Epi& e, int K, hipStream_t st);
 hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                        int64_t ldb, const Epi& e, int64_t K, hipStream_t st);
+bool wldsp_ok(const i8l_config& c, int64_t K);
+hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                        int64_t ldb, const Epi& e, hipStream_t st);
 bool dq_ok(const i8l_config& c, int64_t K);
 bool default_dq_config(int64_t N, int64_t K, i8l_config* c);
 hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,

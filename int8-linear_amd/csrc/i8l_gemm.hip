@@ -134,7 +134,7 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
     return I8L_UNSUPPORTED;
   }
   if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && dmap_index(c) < 0 &&
-      !wlds_ok(c, K)) {
+      !wlds_ok(c, K) && !wldsp_ok(c, K)) {
     set_error("config %dx%dx%d w%d s%d g%d k%d is not built into this library", c.bm, c.bn,
               c.bk, c.warps, c.stages, c.group_m, c.split_k);
     return I8L_UNSUPPORTED;
@@ -218,13 +218,15 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     err = hipGetLastError();
   } else if (c.stages == 1) {
     err = launch_stream(c, a, stride_am, b, stride_bn, e, (int)K, hs);
-  } else if (c.stages == 3 && c.bn <= 32) {
-    // the schedule keeps in-tile row offsets (< 128 token rows, < 32 weight rows) in 32 bits
+  } else if ((c.stages == 3 || c.stages == 4) && c.bn <= 32) {
+    // the schedules keep in-tile row offsets (< 128 token rows, < 32 weight rows) in 32 bits
     if (stride_am > INT32_MAX / 128 || stride_bn > INT32_MAX / 32) {
       const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
       hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
                          stride_bk, stride_bn, e, K);
       err = hipGetLastError();
+    } else if (c.stages == 4) {
+      err = launch_wldsp(c, a, stride_am, b, stride_bn, e, hs);
     } else {
       err = launch_wlds(c, a, stride_am, b, stride_bn, e, K, hs);
     }

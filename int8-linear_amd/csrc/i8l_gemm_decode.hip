@@ -2,6 +2,7 @@
 //  * stream: weights streamed from HBM straight into MFMA operand registers;
 //  * wlds / wlds1: weights copied through LDS with direct-to-LDS loads, K split over the
 //    waves, one or several steps a wave;
+//  * wlds1p: wlds1 walking several column tiles with the activations held in registers;
 //  * wlds1_dq: wlds1 with the per-token activation quantizer folded in.
 // v_mfma_i32_16x16x64_i8 with the weight fragment as srcA and the activations as srcB.
 #include "i8l_gemm.h"
@@ -426,6 +427,121 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
   }
 }
 
+// ------------------------------------------------------------------ persistent single-step decode
+// gemm_wlds1 walking several column tiles: a workgroup loads its token rows' activation
+// fragments into registers once and then takes the column tiles blockIdx.x, blockIdx.x +
+// gridDim.x, ...; each tile's weights are requested into the other of two LDS buffers before
+// the current tile's MFMAs, reduction and epilogue.  gemm_wlds1 reads A (its 16*MT rows,
+// all of K) once per column tile, as much L2 traffic as the weights themselves at 16 tokens;
+// here A is read once per workgroup.  Each wave reads only its own weight slices, so a
+// buffer is refilled as soon as the wave's own MFMAs have consumed it; the reduction area
+// is shared and is fenced by a barrier on each side.
+template <int MT, int NC, int KS, int W, int EK>
+__global__ void __launch_bounds__(64 * W)
+gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
+            int64_t ldb, Epi e) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int SB = NC * S;
+  constexpr int NI = SB / 1024;
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  constexpr int NCF = NC < 16 ? NC : 16;
+  constexpr int NF = NC / NCF;
+  constexpr int FR = MT * NF;
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  static_assert(FR <= W, "every fragment needs a storing wave");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int tiles = e.N / NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)wave * S;
+  int8_t* const wb0 = lds + (size_t)wave * SB;
+  int8_t* const wb1 = lds + (size_t)(W + wave) * SB;
+  v4i* const red = (v4i*)(lds + (size_t)2 * W * SB);  // [W][FR][64]
+  const int ldb32 = (int)ldb;
+
+  auto dma = [&](int ct, int8_t* wb) {
+    const int8_t* Bw = B + (int64_t)ct * NC * ldb + kw;
+    lds_i8_t* dst = (lds_i8_t*)wb;
+#pragma unroll
+    for (int t = 0; t < NI; ++t) {
+      const int o = t * 1024 + 16 * lane;
+      const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+      __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                       16, 0, 0);
+    }
+  };
+
+  const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
+  const int lda32 = (int)lda;
+  v4i a[KS][MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = 16 * i + r16;
+    const int8_t* ap = Aw + (m0 + ml < e.M ? ml * lda32 : 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s][i] = ld16(ap + 64 * s);
+  }
+  const int64_t mrow = m0 + 16 * (wave / NF) + r16;
+  float sam = 0.0f;
+  if (wave < FR) sam = load_sa<EK>(e, mrow < e.M ? mrow : m0);
+
+  int ct = blockIdx.x;
+  dma(ct, wb0);
+  for (int it = 0; ct < tiles; ++it, ct += gridDim.x) {
+    int8_t* const cur = (it & 1) ? wb1 : wb0;
+    const int64_t n0 = (int64_t)ct * NC;
+    const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+    Cols4 cl;
+    if (wave < FR) cl = load_cols4<EK>(e, ncol);
+    const bool more = ct + (int)gridDim.x < tiles;  // uniform over the workgroup
+    if (more) {
+      dma(ct + gridDim.x, (it & 1) ? wb0 : wb1);
+      wait_vmcnt_wlds<NI>();   // everything but the next tile's weights has landed
+    } else {
+      wait_vmcnt_wlds<0>();
+    }
+    v4i b[KS][NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int br = NCF * f + r16 % NCF;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        b[s][f] = *(const v4i*)(cur + br * S + 16 * ((4 * s + grp) ^ (br & SWM)));
+    }
+    v4i acc[MT][NF];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s][i], acc[i][f], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) red[(wave * FR + i * NF + f) * 64 + lane] = acc[i][f];
+    __syncthreads();
+    if (wave < FR) {
+      v4i sum = red[wave * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < W; ++w) sum += red[(w * FR + wave) * 64 + lane];
+      if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
+    }
+    __syncthreads();  // the partials of the next tile overwrite the reduction area
+  }
+}
+
 // ------------------------------------------------------------------ dynamic-quant decode
 // gemm_wlds1 with the per-token activation quantizer folded in, for one 16-token row block.
 // A arrives as the bf16/fp16 X [M, K] that quant_per_token would quantize; each wave
@@ -749,6 +865,83 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
   I8L_WLDS(1, 32, 2) I8L_WLDS(1, 32, 4) I8L_WLDS(2, 32, 2) I8L_WLDS(2, 32, 4)
   I8L_WLDS(4, 32, 2) I8L_WLDS(4, 32, 4)
 #undef I8L_WLDS
+  return hipErrorInvalidValue;
+}
+
+// Persistent single-step tiles (stages 4): (MT, NC, KS, W), K = 64 * KS * W.  Two weight
+// buffers and the reduction area must fit the LDS; W = 16 needs MT * KS <= 6 (registers).
+struct WldsPTile {
+  int mt, nc, ks, w;
+};
+constexpr WldsPTile kWldsP[] = {{1, 16, 2, 16}, {2, 16, 2, 16}, {1, 32, 2, 16}, {1, 16, 4, 16},
+                                {1, 16, 4, 8},  {2, 16, 4, 8},  {4, 16, 4, 8},  {1, 16, 8, 8}};
+
+size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
+  const int nf = nc > 16 ? nc / 16 : 1;
+  return (size_t)2 * w * nc * 64 * ks + (size_t)w * mt * nf * 1024;
+}
+
+bool wldsp_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 4 || c.split_k != 1 || c.bn > 32) return false;
+  for (auto t : kWldsP)
+    if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
+      return K == (int64_t)c.bk * c.warps && wldsp_lds_bytes(t.mt, t.nc, t.ks, t.w) <= kMaxLds;
+  return false;
+}
+
+// Compute units of the current device (cached per device; 256 if the query fails).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+template <int MT, int NC, int KS, int W, int EK>
+hipError_t launch_wldsp_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  auto kern = gemm_wlds1p<MT, NC, KS, W, EK>;
+  const size_t shm = wldsp_lds_bytes(MT, NC, KS, W);
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
+  const int rows = (e.M + 16 * MT - 1) / (16 * MT);
+  const int tiles = e.N / NC;
+  const int per_row = std::max(1, cu_count() / rows);  // one workgroup a compute unit
+  const dim3 grid((unsigned)std::min(tiles, per_row), (unsigned)rows);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
+  return hipGetLastError();
+}
+
+template <int MT, int NC, int KS, int W>
+hipError_t launch_wldsp_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                          const Epi& e, hipStream_t st) {
+  switch (epi_kind(e)) {
+    case EK_BF16: return launch_wldsp_k<MT, NC, KS, W, EK_BF16>(a, lda, b, ldb, e, st);
+    case EK_BF16_BBF16: return launch_wldsp_k<MT, NC, KS, W, EK_BF16_BBF16>(a, lda, b, ldb, e, st);
+    default: return launch_wldsp_k<MT, NC, KS, W, EK_ANY>(a, lda, b, ldb, e, st);
+  }
+}
+
+hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                        int64_t ldb, const Epi& e, hipStream_t st) {
+  const int mt = c.bm / 16, nc = c.bn, ks = c.bk / 64, w = c.warps;
+#define I8L_WLDSP(MT_, NC_, KS_, W_)                                                        \
+  if (mt == MT_ && nc == NC_ && ks == KS_ && w == W_)                                        \
+    return launch_wldsp_t<MT_, NC_, KS_, W_>(a, lda, b, ldb, e, st);
+  I8L_WLDSP(1, 16, 2, 16) I8L_WLDSP(2, 16, 2, 16) I8L_WLDSP(1, 32, 2, 16) I8L_WLDSP(1, 16, 4, 16)
+  I8L_WLDSP(1, 16, 4, 8) I8L_WLDSP(2, 16, 4, 8) I8L_WLDSP(4, 16, 4, 8) I8L_WLDSP(1, 16, 8, 8)
+#undef I8L_WLDSP
   return hipErrorInvalidValue;
 }
 

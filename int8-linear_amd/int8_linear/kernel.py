@@ -39,8 +39,10 @@ class Config:
     Decode schedules (bm <= 128 tokens a workgroup, bn <= 32 columns):
       stages == 1: weights streamed into MFMA registers; `warps` waves split K in 64-byte
         steps, so bk == 64 * warps.
-      stages == 3, bm <= 32: weights copied through LDS with direct-to-LDS loads; each of the
+      stages == 3: weights copied through LDS with direct-to-LDS loads; each of the
         `warps` waves owns one K slice taken bk bytes per step (K a multiple of bk * warps).
+      stages == 4: the same with one K step a wave (K == bk * warps), each workgroup walking
+        several column tiles with its activations held in registers.
     Prefill schedules (bm x bn macro tiles of 64 to 256, K in bk-byte steps, `group_m`
     rows of tiles walked together):
       stages == 2: double-buffered LDS staged through registers;

@@ -73,6 +73,10 @@ def test_every_tuner_candidate_tile_is_built():
         assert kernel.supported(1024, n, k, Config(bm, bn, bk, w, st, 1)), (bm, bn, bk, st)
     for bm, bn, bk, w in tune.STAGED_TILES:
         assert kernel.supported(1024, n, k, Config(bm, bn, bk, w, 2, 1)), (bm, bn, bk)
+    for mt, nc, ks, w in tune.WLDSP_TILES:                  # persistent: one K step a wave
+        assert kernel.supported(16 * mt, n, w * 64 * ks, Config(16 * mt, nc, 64 * ks, w, 4, 1))
+        assert not kernel.supported(16 * mt, n, 2 * w * 64 * ks,
+                                    Config(16 * mt, nc, 64 * ks, w, 4, 1))
     for mt, nc, ks in tune.WLDS_TILES:                     # one or more K steps a wave
         assert any(kernel.supported(16 * mt, n, steps * w * 64 * ks,
                                     Config(16 * mt, nc, 64 * ks, w, 3, 1))

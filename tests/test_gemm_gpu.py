@@ -156,6 +156,7 @@ def test_every_decode_tile_is_repeatable(m):
                for w_ in (4, 8, 16)]
     configs += [Config(16 * mt, bn, 64 * w_, w_, 1, 1) for mt, bn in tune.STREAM_TILES
                 for w_ in (1, 2, 4, 8, 16)]
+    configs += [Config(16 * mt, nc, 64 * ks, w_, 4, 1) for mt, nc, ks, w_ in tune.WLDSP_TILES]
     checked = 0
     for config in configs:
         if not kernel.supported(m, n, k, config):
@@ -166,6 +167,33 @@ def test_every_decode_tile_is_repeatable(m):
         assert all(torch.equal(o, outs[0]) for o in outs), config.name
         checked += 1
     assert checked >= 40
+
+
+# The persistent single-step decode schedule (stages 4): every built tile on a shape with more
+# column tiles than the launch has workgroups a row block (so each workgroup walks several,
+# and the last walk is ragged), ragged M over one to three row blocks, every epilogue kind.
+WLDSP = [(mt, nc, ks, w) for mt, nc, ks, w in
+         [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
+          (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8)]]
+
+
+@pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
+@pytest.mark.parametrize("m", [1, 17, 40])
+def test_persistent_decode_tiles_exact(mt, nc, ks, w, m):
+    k, n = 64 * ks * w, 32 * 311                          # 622 or 311 column tiles
+    config = Config(16 * mt, nc, 64 * ks, w, 4, 1)
+    say(f"w8a8_mm persistent m={m} k={k} n={n} config={config.name}")
+    a, wt = ints((m, k), 21 + m), ints((n, k), 22)
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, wt.t(), one, one, raw=True, config=config)
+    assert np.array_equal(np_(got), o.gemm_i32(np_(a), np_(wt)))
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    for dtype, bias in ((torch.bfloat16, None),
+                        (torch.bfloat16, (torch.randn(n, device="cuda") * 0.01).to(torch.bfloat16)),
+                        (torch.float16, torch.randn(n, device="cuda") * 0.01)):
+        out = w8a8_mm(a, wt.t(), sa, sb, dtype, bias, config=config)
+        assert np.array_equal(bits(out), oracle_out(a, wt, sa, sb, bias, dtype)), (dtype, bias is None)
 
 
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
