@@ -869,12 +869,14 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
 }
 
 // Persistent single-step tiles (stages 4): (MT, NC, KS, W), K = 64 * KS * W.  Two weight
-// buffers and the reduction area must fit the LDS; W = 16 needs MT * KS <= 6 (registers).
+// buffers and the reduction area must fit the LDS, and the activation fragments (4*KS*MT
+// VGPRs) with the rest of a wave's state the register file (128 VGPRs at W = 16).
 struct WldsPTile {
   int mt, nc, ks, w;
 };
 constexpr WldsPTile kWldsP[] = {{1, 16, 2, 16}, {2, 16, 2, 16}, {1, 32, 2, 16}, {1, 16, 4, 16},
-                                {1, 16, 4, 8},  {2, 16, 4, 8},  {4, 16, 4, 8},  {1, 16, 8, 8}};
+                                {1, 16, 4, 8},  {2, 16, 4, 8},  {4, 16, 4, 8},  {1, 16, 8, 8},
+                                {4, 16, 2, 16}, {8, 16, 4, 8},  {4, 32, 2, 8}};
 
 size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
   const int nf = nc > 16 ? nc / 16 : 1;
@@ -941,6 +943,7 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
     return launch_wldsp_t<MT_, NC_, KS_, W_>(a, lda, b, ldb, e, st);
   I8L_WLDSP(1, 16, 2, 16) I8L_WLDSP(2, 16, 2, 16) I8L_WLDSP(1, 32, 2, 16) I8L_WLDSP(1, 16, 4, 16)
   I8L_WLDSP(1, 16, 4, 8) I8L_WLDSP(2, 16, 4, 8) I8L_WLDSP(4, 16, 4, 8) I8L_WLDSP(1, 16, 8, 8)
+  I8L_WLDSP(4, 16, 2, 16) I8L_WLDSP(8, 16, 4, 8) I8L_WLDSP(4, 32, 2, 8)
 #undef I8L_WLDSP
   return hipErrorInvalidValue;
 }

@@ -174,11 +174,12 @@ def test_every_decode_tile_is_repeatable(m):
 # and the last walk is ragged), ragged M over one to three row blocks, every epilogue kind.
 WLDSP = [(mt, nc, ks, w) for mt, nc, ks, w in
          [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
-          (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8)]]
+          (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
+          (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8)]]
 
 
 @pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
-@pytest.mark.parametrize("m", [1, 17, 40])
+@pytest.mark.parametrize("m", [1, 17, 40, 100])
 def test_persistent_decode_tiles_exact(mt, nc, ks, w, m):
     k, n = 64 * ks * w, 32 * 311                          # 622 or 311 column tiles
     config = Config(16 * mt, nc, 64 * ks, w, 4, 1)
