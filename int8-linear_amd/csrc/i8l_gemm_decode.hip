@@ -876,18 +876,24 @@ struct WldsPTile {
 };
 constexpr WldsPTile kWldsP[] = {{1, 16, 2, 16}, {2, 16, 2, 16}, {1, 32, 2, 16}, {1, 16, 4, 16},
                                 {1, 16, 4, 8},  {2, 16, 4, 8},  {4, 16, 4, 8},  {1, 16, 8, 8},
-                                {4, 16, 2, 16}, {8, 16, 4, 8},  {4, 32, 2, 8}};
+                                {4, 16, 2, 16}, {8, 16, 4, 8},  {4, 32, 2, 8},  {1, 8, 2, 16},
+                                {1, 8, 4, 16},  {1, 8, 8, 8}};
 
 size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
   const int nf = nc > 16 ? nc / 16 : 1;
   return (size_t)2 * w * nc * 64 * ks + (size_t)w * mt * nf * 1024;
 }
 
+// group_m is the number of workgroups a compute unit runs at once (1 or 2): both must fit
+// its LDS and its 2048 threads.
 bool wldsp_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 4 || c.split_k != 1 || c.bn > 32) return false;
+  if (c.stages != 4 || c.split_k != 1 || c.bn > 32 || c.group_m < 1 || c.group_m > 2)
+    return false;
   for (auto t : kWldsP)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
-      return K == (int64_t)c.bk * c.warps && wldsp_lds_bytes(t.mt, t.nc, t.ks, t.w) <= kMaxLds;
+      return K == (int64_t)c.bk * c.warps &&
+             (size_t)c.group_m * wldsp_lds_bytes(t.mt, t.nc, t.ks, t.w) <= kMaxLds &&
+             c.group_m * 64 * t.w <= 2048;
   return false;
 }
 
@@ -912,14 +918,14 @@ int cu_count() {
 
 template <int MT, int NC, int KS, int W, int EK>
 hipError_t launch_wldsp_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
-                          const Epi& e, hipStream_t st) {
+                          const Epi& e, int per_cu, hipStream_t st) {
   auto kern = gemm_wlds1p<MT, NC, KS, W, EK>;
   const size_t shm = wldsp_lds_bytes(MT, NC, KS, W);
   static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
   lds_opt_in((const void*)kern, shm, lds_done);
   const int rows = (e.M + 16 * MT - 1) / (16 * MT);
   const int tiles = e.N / NC;
-  const int per_row = std::max(1, cu_count() / rows);  // one workgroup a compute unit
+  const int per_row = std::max(1, per_cu * cu_count() / rows);  // per_cu workgroups a CU
   const dim3 grid((unsigned)std::min(tiles, per_row), (unsigned)rows);
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
   return hipGetLastError();
@@ -927,11 +933,12 @@ hipError_t launch_wldsp_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t
 
 template <int MT, int NC, int KS, int W>
 hipError_t launch_wldsp_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
-                          const Epi& e, hipStream_t st) {
+                          const Epi& e, int per_cu, hipStream_t st) {
   switch (epi_kind(e)) {
-    case EK_BF16: return launch_wldsp_k<MT, NC, KS, W, EK_BF16>(a, lda, b, ldb, e, st);
-    case EK_BF16_BBF16: return launch_wldsp_k<MT, NC, KS, W, EK_BF16_BBF16>(a, lda, b, ldb, e, st);
-    default: return launch_wldsp_k<MT, NC, KS, W, EK_ANY>(a, lda, b, ldb, e, st);
+    case EK_BF16: return launch_wldsp_k<MT, NC, KS, W, EK_BF16>(a, lda, b, ldb, e, per_cu, st);
+    case EK_BF16_BBF16:
+      return launch_wldsp_k<MT, NC, KS, W, EK_BF16_BBF16>(a, lda, b, ldb, e, per_cu, st);
+    default: return launch_wldsp_k<MT, NC, KS, W, EK_ANY>(a, lda, b, ldb, e, per_cu, st);
   }
 }
 
@@ -940,10 +947,11 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
   const int mt = c.bm / 16, nc = c.bn, ks = c.bk / 64, w = c.warps;
 #define I8L_WLDSP(MT_, NC_, KS_, W_)                                                        \
   if (mt == MT_ && nc == NC_ && ks == KS_ && w == W_)                                        \
-    return launch_wldsp_t<MT_, NC_, KS_, W_>(a, lda, b, ldb, e, st);
+    return launch_wldsp_t<MT_, NC_, KS_, W_>(a, lda, b, ldb, e, c.group_m, st);
   I8L_WLDSP(1, 16, 2, 16) I8L_WLDSP(2, 16, 2, 16) I8L_WLDSP(1, 32, 2, 16) I8L_WLDSP(1, 16, 4, 16)
   I8L_WLDSP(1, 16, 4, 8) I8L_WLDSP(2, 16, 4, 8) I8L_WLDSP(4, 16, 4, 8) I8L_WLDSP(1, 16, 8, 8)
-  I8L_WLDSP(4, 16, 2, 16) I8L_WLDSP(8, 16, 4, 8) I8L_WLDSP(4, 32, 2, 8)
+  I8L_WLDSP(4, 16, 2, 16) I8L_WLDSP(8, 16, 4, 8) I8L_WLDSP(4, 32, 2, 8) I8L_WLDSP(1, 8, 2, 16)
+  I8L_WLDSP(1, 8, 4, 16) I8L_WLDSP(1, 8, 8, 8)
 #undef I8L_WLDSP
   return hipErrorInvalidValue;
 }

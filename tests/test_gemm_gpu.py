@@ -175,14 +175,16 @@ def test_every_decode_tile_is_repeatable(m):
 WLDSP = [(mt, nc, ks, w) for mt, nc, ks, w in
          [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
           (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
-          (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8)]]
+          (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8), (1, 8, 2, 16), (1, 8, 4, 16),
+          (1, 8, 8, 8)]]
 
 
 @pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
 @pytest.mark.parametrize("m", [1, 17, 40, 100])
 def test_persistent_decode_tiles_exact(mt, nc, ks, w, m):
     k, n = 64 * ks * w, 32 * 311                          # 622 or 311 column tiles
-    config = Config(16 * mt, nc, 64 * ks, w, 4, 1)
+    config = Config(16 * mt, nc, 64 * ks, w, 4, 2 if kernel.supported(m, 32 * 311, k, Config(
+        16 * mt, nc, 64 * ks, w, 4, 2)) and m % 2 else 1)   # two workgroups a CU where they fit
     say(f"w8a8_mm persistent m={m} k={k} n={n} config={config.name}")
     a, wt = ints((m, k), 21 + m), ints((n, k), 22)
     one = torch.ones(1, device="cuda")
