@@ -54,7 +54,7 @@ enum {
  *                same ring of stages - 8 buffers with fragment reads overlapped with the
  *                MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); with
- *                stages 4, the workgroups a compute unit runs at once (1 or 2)
+ *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4)
  *   split_k    : reserved; must be 1
  * A config the library was not built for returns I8L_UNSUPPORTED.
  */

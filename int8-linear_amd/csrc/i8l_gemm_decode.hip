@@ -877,17 +877,19 @@ struct WldsPTile {
 constexpr WldsPTile kWldsP[] = {{1, 16, 2, 16}, {2, 16, 2, 16}, {1, 32, 2, 16}, {1, 16, 4, 16},
                                 {1, 16, 4, 8},  {2, 16, 4, 8},  {4, 16, 4, 8},  {1, 16, 8, 8},
                                 {4, 16, 2, 16}, {8, 16, 4, 8},  {4, 32, 2, 8},  {1, 8, 2, 16},
-                                {1, 8, 4, 16},  {1, 8, 8, 8}};
+                                {1, 8, 4, 16},  {1, 8, 8, 8},   {1, 8, 16, 4},  {1, 16, 16, 4},
+                                {1, 8, 8, 4},   {1, 16, 8, 4}};
 
 size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
   const int nf = nc > 16 ? nc / 16 : 1;
   return (size_t)2 * w * nc * 64 * ks + (size_t)w * mt * nf * 1024;
 }
 
-// group_m is the number of workgroups a compute unit runs at once (1 or 2): both must fit
-// its LDS and its 2048 threads.
+// group_m is the number of workgroups a compute unit runs at once (1, 2 or 4): all of them
+// must fit its LDS and its 2048 threads.
 bool wldsp_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 4 || c.split_k != 1 || c.bn > 32 || c.group_m < 1 || c.group_m > 2)
+  if (c.stages != 4 || c.split_k != 1 || c.bn > 32 ||
+      (c.group_m != 1 && c.group_m != 2 && c.group_m != 4))
     return false;
   for (auto t : kWldsP)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
@@ -951,7 +953,8 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
   I8L_WLDSP(1, 16, 2, 16) I8L_WLDSP(2, 16, 2, 16) I8L_WLDSP(1, 32, 2, 16) I8L_WLDSP(1, 16, 4, 16)
   I8L_WLDSP(1, 16, 4, 8) I8L_WLDSP(2, 16, 4, 8) I8L_WLDSP(4, 16, 4, 8) I8L_WLDSP(1, 16, 8, 8)
   I8L_WLDSP(4, 16, 2, 16) I8L_WLDSP(8, 16, 4, 8) I8L_WLDSP(4, 32, 2, 8) I8L_WLDSP(1, 8, 2, 16)
-  I8L_WLDSP(1, 8, 4, 16) I8L_WLDSP(1, 8, 8, 8)
+  I8L_WLDSP(1, 8, 4, 16) I8L_WLDSP(1, 8, 8, 8) I8L_WLDSP(1, 8, 16, 4) I8L_WLDSP(1, 16, 16, 4)
+  I8L_WLDSP(1, 8, 8, 4) I8L_WLDSP(1, 16, 8, 4)
 #undef I8L_WLDSP
   return hipErrorInvalidValue;
 }

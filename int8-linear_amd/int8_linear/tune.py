@@ -62,7 +62,7 @@ DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
 WLDSP_TILES = [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
                (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
                (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8), (1, 8, 2, 16), (1, 8, 4, 16),
-               (1, 8, 8, 8)]
+               (1, 8, 8, 8), (1, 8, 16, 4), (1, 16, 16, 4), (1, 8, 8, 4), (1, 16, 8, 4)]
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
 WLDS_TILES = [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
@@ -94,7 +94,7 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
         for mt, nc, ks, w in WLDSP_TILES:
             if mt > need:
                 continue
-            for g in (1, 2):                 # workgroups a compute unit
+            for g in (1, 2, 4):              # workgroups a compute unit
                 cfg = Config(16 * mt, nc, 64 * ks, w, 4, g)
                 if supported(m, n, k, cfg):
                     out.append(cfg)
