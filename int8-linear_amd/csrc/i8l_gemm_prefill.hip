@@ -17,6 +17,61 @@ namespace i8l {
 template <int BM, int BN, int WM, int WN>
 constexpr int tile_epilogue_lds_bytes() { return BM * (2 * BN + 16); }
 
+// The scales and bias of a wave's FA x 4 column quads (column n = nb + 32a + 8q), every load
+// issued before any is used: one memory round trip.  BD (the bias dtype) and SBC (per-column
+// scale_b) are fixed per specialization, so no branch separates the loads.
+template <int FA, int BD, bool SBC>
+__device__ __forceinline__ void load_tile_cols_k(const Epi& e, int64_t nb, Cols4 (&cl)[FA][4]) {
+  float4 sbv[FA][4];
+  float sb0 = 0.0f;
+  uint2 bh[FA][4];
+  float4 bf[FA][4];
+#pragma unroll
+  for (int a = 0; a < FA; ++a)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = nb + 32 * a + 8 * q;
+      if constexpr (SBC) sbv[a][q] = *(const float4*)(e.sb + n);
+      if constexpr (BD == I8L_F32) bf[a][q] = *(const float4*)((const float*)e.bias + n);
+      if constexpr (BD == I8L_BF16 || BD == I8L_F16)
+        bh[a][q] = *(const uint2*)((const uint16_t*)e.bias + n);
+    }
+  if constexpr (!SBC) sb0 = e.sb[0];
+#pragma unroll
+  for (int a = 0; a < FA; ++a)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      Cols4& c = cl[a][q];
+      if constexpr (SBC) {
+        c.sb[0] = sbv[a][q].x, c.sb[1] = sbv[a][q].y, c.sb[2] = sbv[a][q].z, c.sb[3] = sbv[a][q].w;
+      } else {
+        c.sb[0] = c.sb[1] = c.sb[2] = c.sb[3] = sb0;
+      }
+      if constexpr (BD == I8L_F32) {
+        c.bias[0] = bf[a][q].x, c.bias[1] = bf[a][q].y, c.bias[2] = bf[a][q].z,
+        c.bias[3] = bf[a][q].w;
+      } else if constexpr (BD == I8L_BF16 || BD == I8L_F16) {
+        const uint32_t w[4] = {bh[a][q].x & 0xffffu, bh[a][q].x >> 16, bh[a][q].y & 0xffffu,
+                               bh[a][q].y >> 16};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          c.bias[r] = BD == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
+      } else {
+        c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = 0.0f;
+      }
+    }
+}
+
+template <int FA, bool SBC>
+__device__ __forceinline__ void load_tile_cols_s(const Epi& e, int64_t nb, Cols4 (&cl)[FA][4]) {
+  switch (e.bias_dtype) {
+    case I8L_DTYPE_NONE: load_tile_cols_k<FA, I8L_DTYPE_NONE, SBC>(e, nb, cl); break;
+    case I8L_BF16: load_tile_cols_k<FA, I8L_BF16, SBC>(e, nb, cl); break;
+    case I8L_F16: load_tile_cols_k<FA, I8L_F16, SBC>(e, nb, cl); break;
+    default: load_tile_cols_k<FA, I8L_F32, SBC>(e, nb, cl); break;
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int FA, int FB>
 __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB], int8_t* lds,
                                               int64_t m0, int64_t n0, int wm, int wn, int lane,
@@ -49,11 +104,14 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
     sam[b] = load_sa(e, m < e.M ? m : 0);
   }
   const bool bf = e.out_dtype == I8L_BF16;
+  Cols4 cls[FA][4];
+  if (e.sb_per_col)
+    load_tile_cols_s<FA, true>(e, n0 + wn * TN + 4 * fhalf, cls);
+  else
+    load_tile_cols_s<FA, false>(e, n0 + wn * TN + 4 * fhalf, cls);
 #pragma unroll
   for (int a = 0; a < FA; ++a) {
-    Cols4 cl[4];  // one 32-column fragment's scales and bias at a time
-#pragma unroll
-    for (int q = 0; q < 4; ++q) cl[q] = load_cols4(e, n0 + wn * TN + a * 32 + 8 * q + 4 * fhalf);
+    const Cols4 (&cl)[4] = cls[a];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = wn * TN + a * 32 + 8 * q + 4 * fhalf;  // column within the tile
