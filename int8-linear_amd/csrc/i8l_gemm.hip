@@ -24,9 +24,19 @@ gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_
 void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   *c = i8l_config{0, 0, 0, 0, 0, 1, 1};
   if (M <= 32 && K % 128 == 0) {
+    const int mt = M <= 16 ? 1 : 2;
+    // Many column tiles (N/16 >= 512) from 9 tokens: the persistent single-step tile with two
+    // workgroups a CU, which loads the activations once a workgroup instead of once a tile.
+    if (M > 8 && N % 16 == 0 && N / 16 >= 512) {
+      const i8l_config p = K == 4096 ? i8l_config{16 * mt, 8, 512, 8, 4, 2, 1}
+                                     : i8l_config{16 * mt, 16, 256, 8, 4, 2, 1};
+      if (wldsp_ok(p, K)) {
+        *c = p;
+        return;
+      }
+    }
     // weights through LDS: 16 (or, for narrow N, 8) columns a workgroup, the K split over
     // up to 16 waves in one or more steps of up to 512 bytes
-    const int mt = M <= 16 ? 1 : 2;
     const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : (N % 8 == 0 ? 8 : 4);
     const int64_t k64 = K / 64;
     const int kss[] = {8, 6, 4, 2};

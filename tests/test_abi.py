@@ -52,6 +52,12 @@ def test_default_config_regimes():
     p = default_config(4096, 28672, 4096)
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
     assert default_config(300, 2048, 2048).stages >= 2
+    # 9-32 tokens on many column tiles: the persistent tile, two workgroups a CU
+    assert default_config(16, 12288, 2048) == Config(16, 16, 256, 8, 4, 2)
+    assert default_config(24, 12288, 2048) == Config(32, 16, 256, 8, 4, 2)
+    assert default_config(16, 28672, 4096) == Config(16, 8, 512, 8, 4, 2)
+    assert default_config(4, 12288, 2048).stages == 3     # few tokens: A is small
+    assert default_config(24, 28672, 4096).stages == 3    # no 32-row 8-column persistent tile
     mid = default_config(96, 12288, 2048)                   # 64-token overlapped-ring tiles
     assert (mid.bm, mid.bn, mid.stages) == (64, 64, 12)
     assert (default_config(512, 4096, 4096).bm, default_config(512, 4096, 4096).bn) == (128, 64)
