@@ -153,6 +153,32 @@ def test_silu_mul_quant_extreme_gates(i, m):
     check_silu(torch.nan_to_num(gh, neginf=-65504.0), True)
 
 
+@pytest.mark.parametrize("i,m", [(2048, 40), (6144, 1000), (6144, 4100)])
+def test_silu_mul_quant_every_bf16_gate(i, m):
+    """The gates of the first rows run through every bf16 value with |g| < 2^124 (both signs,
+    zeros, subnormals), so the fast quotient (rcp and one Newton-Markstein step) and the
+    IEEE-division path for gates at or below -87 each meet every gate they can get; the other
+    rows are random.  (Above 2^124, silu(g)*u can overflow to inf, and a code computed from an
+    infinite absmax is outside the bit-exact contract.)  Three row geometries, ragged M."""
+    say(f"silu_mul_quant every bf16 gate i={i} m={m}")
+    g = torch.Generator().manual_seed(i + m)
+    gate = (torch.randn((m, i), generator=g) * 2.0).to(torch.bfloat16)
+    up = torch.randn((m, i), generator=g).to(torch.bfloat16)
+    pats = np.arange(1 << 16, dtype=np.uint32)
+    pats = pats[((pats >> 7) & 0xff) <= 250].astype(np.uint16)
+    gb = bits(gate).copy()
+    gb.reshape(-1)[:pats.size] = pats
+    gu = torch.cat([from_bits(gb, device="cpu"), up], dim=1).cuda()
+    for rs in (False, True):
+        for precise in (True, False):
+            q, s = fq.silu_mul_quant(gu, precise_div=precise, round_silu=rs)
+            q0, s0 = o.silu_mul_quant(bits(gu), o.BF16, rs, precise)
+            bad = np.argwhere(np_(q) != q0)[:5]
+            assert bad.size == 0, [(int(r), int(c), hex(gb[r, c]), int(np_(q)[r, c]), int(q0[r, c]))
+                                   for r, c in bad]
+            assert np.array_equal(np_(s), s0), np.argwhere(np_(s) != s0)[:5]
+
+
 @pytest.mark.parametrize("m", [1, 16, 128, 1024, 4096])
 def test_silu_mul_quant_config2(m):
     say(f"silu_mul_quant config2 m={m}")
