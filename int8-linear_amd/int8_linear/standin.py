@@ -52,6 +52,8 @@ class DecoderStandIn:
         g = torch.Generator(device=generator_device).manual_seed(seed)
         dev = torch.device(device)
         self.m = m
+        # per-linear configurations ({name: Config}); a linear not named takes choose_config
+        self.configs: dict = {}
         self.x = torch.randn((m, HIDDEN), generator=g, device=generator_device).to(
             torch.bfloat16).to(dev)
         self.norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
@@ -85,7 +87,7 @@ class DecoderStandIn:
 
     def mm(self, layer, name: str, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
         w, ws = layer[name]
-        return w8a8_mm(q, w.t(), s, ws, torch.bfloat16)
+        return w8a8_mm(q, w.t(), s, ws, torch.bfloat16, config=self.configs.get(name))
 
     def forward(self) -> torch.Tensor:
         """One step through every layer; returns the last down_proj output [m, HIDDEN]."""
