@@ -14,8 +14,10 @@ in the 256 MiB Infinity Cache.  `value` is the mean microseconds per linear over
 After the timed steps (not inside them): per-call graph-replay times of every sweep point,
 the roofline object of the dominant kernel (HIP events on the launch stream, algorithmic
 bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3), the
-28-layer decoder stand-in in microseconds per layer (config 4), and the CPU baseline (the
-oracle's CPU restatement of the reference's path, on a bounded sample).
+28-layer decoder stand-in in microseconds per layer (config 4), the CPU baseline (the
+oracle's CPU restatement of the reference's path, on a bounded sample) and, beside it, the
+reference's own CPU path as torch ops (`cpu_reference_path`: torch._int_mm and an int32
+matmul with the fp32 dequant for config 0, the torch quantizers at 1024 tokens).
 
     python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
     python bench.py --only standin       # one extra section alone
@@ -233,6 +235,66 @@ def cpu_baseline() -> dict:
                       f"(int32 GEMM + fp32 dequant), OpenMP threads={threads}"}
 
 
+def cpu_reference_path(seconds: float = 2.0) -> dict:
+    """The reference's CPU path as torch ops on the host cores (each leg repeated for about
+    `seconds`): the int32 product of config 0 by torch's int8 matmul (torch._int_mm) and by
+    an int32 matmul, each with the fp32 dequant and bf16 cast (kernel.py:105-120); and the
+    reference's torch restatements of the fused quantizers (tests/test_fused_quant.py:26-51)
+    at config 2's 1024 tokens.  Reported beside the oracle's time, not as a target."""
+    import torch
+
+    from int8_linear.operands import operands, seed_of
+
+    def per_call_us(fn) -> tuple[float, int]:
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or reps < 3:
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps * 1e6, reps
+
+    m, k, n = 16, 2048, 4096
+    d = operands(m, k, n, seed_of(m, k, n))
+    a, w, sa, sb = d["a_q"], d["w_q"], d["a_s"], d["w_s"].view(1, -1)
+
+    def dequant(acc):
+        return (acc.float() * sa * sb).to(torch.bfloat16)
+
+    def quant(yf):
+        absmax = yf.abs().amax(-1, keepdim=True)
+        inv = torch.where(absmax == 0, torch.zeros_like(absmax), 127.0 / absmax)
+        return torch.round(yf * inv).clamp(-128, 127).to(torch.int8), absmax / 127.0
+
+    g = torch.Generator().manual_seed(1)
+    mq, h, inter = 1024, 2048, 6144
+    x = torch.randn((mq, h), generator=g).to(torch.bfloat16)
+    r = torch.randn((mq, h), generator=g).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    gu = torch.randn((mq, 2 * inter), generator=g).to(torch.bfloat16)
+
+    def norm():
+        xf = x.float() + r.float()
+        var = xf.pow(2).mean(-1, keepdim=True)
+        y = ((xf * torch.rsqrt(var + 1e-6)).to(gamma.dtype) * gamma).to(x.dtype)
+        return quant(y.float()), xf.to(x.dtype)
+
+    def silu():
+        gf, uf = gu[:, :inter].float(), gu[:, inter:].float()
+        act = (gf / (1.0 + torch.exp(-gf))).to(gu.dtype).float()
+        return quant((act * uf).to(gu.dtype).float())
+
+    legs = {"gemm_int_mm": lambda: dequant(torch._int_mm(a, w.t())),
+            "gemm_int32_matmul": lambda: dequant(a.int() @ w.int().t()),
+            "add_rmsnorm_quant": norm, "silu_mul_quant": silu}
+    out = {"unit": "us per call", "threads": torch.get_num_threads(),
+           "sample": f"config 0 GEMM (M=16, K=2048, N=4096) and config 2 quantizers at M={mq} "
+                     f"(H={h}, I={inter}), torch CPU ops, about {seconds:g} s a leg"}
+    for name, fn in legs.items():
+        us, reps = per_call_us(fn)
+        out[name] = round(us, 2)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,6 +409,7 @@ def main() -> int:
         result["launch"] = bench_launch(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+        result["cpu_reference_path"] = cpu_reference_path()
     print(json.dumps(result), flush=True)
     return 0
 
