@@ -586,7 +586,8 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {64, 128, 128, 2, 2, 6}, {64, 64, 128, 2, 2, 4},
                              {128, 64, 128, 2, 2, 4}, {128, 384, 64, 2, 4, 3},
                              {128, 384, 64, 2, 4, 4}, {128, 192, 64, 2, 2, 4},
-                             {256, 192, 64, 2, 2, 4}};
+                             {256, 192, 64, 2, 2, 4}, {64, 192, 64, 2, 2, 4},
+                             {64, 192, 128, 2, 2, 4}};
 
 int dmap_index(const i8l_config& c) {
   if (c.stages < 3 + kPipelined || c.split_k != 1 || c.group_m < 1) return -1;
@@ -698,6 +699,8 @@ hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t ld
     case 16: return launch_dmap_t<128, 384, 64, 2, 4, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 17: return launch_dmap_t<128, 192, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 18: return launch_dmap_t<256, 192, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 19: return launch_dmap_t<64, 192, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 20: return launch_dmap_t<64, 192, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }
