@@ -227,3 +227,24 @@ def test_dynamic_quant_entry_validates_on_the_host():
     assert L.i8l_w8a8_mm_dynq(*args) == _lib.UNSUPPORTED
     args[2], args[15] = _lib.BF16, 0                            # M == 0: nothing to do
     assert L.i8l_w8a8_mm_dynq(*args) == _lib.OK
+
+
+def test_situ_tune_writes_only_kept_sets_as_table_rows():
+    """The in-situ tuner's table rows (reference bench/situ_tune.py:241-246): nothing for a
+    set that was not kept; for a kept set, one row per linear at the batch, each with its
+    configuration and the confirmed stand-in time."""
+    from dataclasses import asdict
+
+    from int8_linear import situ_tune
+    from int8_linear.standin import SHAPES
+
+    cfg = asdict(Config(16, 16, 256, 8, 4, 2))
+    entry = {"batch": 8, "chosen": {name: cfg for name in SHAPES}, "kept": False,
+             "confirm_us": {"start": 31.0, "chosen": 30.9}}
+    assert situ_tune.table_rows(entry) == {}
+    entry["kept"] = True
+    rows = situ_tune.table_rows(entry)
+    assert set(rows) == {f"{k}x{n}" for k, n in SHAPES.values()}
+    for r in rows.values():
+        assert r == {"8": {"config": cfg, "stand_in_us": 30.9}}
+    assert 0 < situ_tune.ACCEPT < 0.05
