@@ -29,7 +29,7 @@ from __future__ import annotations
 import torch
 
 from int8_linear import _lib
-from int8_linear.kernel import NotSupported
+from int8_linear.kernel import NotSupported, same_device
 
 _ACT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -68,6 +68,7 @@ def add_rmsnorm_quant(x: torch.Tensor, residual: torch.Tensor | None, weight: to
     if weight.numel() != K:
         raise ValueError(f"weight has {weight.numel()} values for rows of {K}")
     weight = weight.contiguous()
+    same_device(x.device, weight=weight, residual=residual)
     if residual is not None:
         assert residual.is_contiguous() and residual.shape == x.shape
         if residual.dtype != x.dtype:
@@ -153,6 +154,7 @@ def quant_mm(x: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
     act = _act_code(x, "x")
     if b_q.dtype != torch.int8 or not b_q.is_cuda:
         raise NotSupported("b_q must be an int8 HIP tensor")
+    same_device(x.device, b_q=b_q, scale_b=scale_b, bias=bias)
     M, K = x.shape
     N = b_q.shape[1]
     if M > QUANT_MM_MAX_M:

@@ -154,6 +154,13 @@ def _fast_mm(a_q, b_q, scale_a, scale_b, out_dtype, bias):
     return out
 
 
+def same_device(device: torch.device, **tensors) -> None:
+    """Raise ValueError unless every tensor given (None entries are skipped) is on `device`."""
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise ValueError(f"{name} is on {t.device}, the launch is on {device}")
+
+
 def supported(m: int, n: int, k: int, config: Config | None = None) -> bool:
     """Whether w8a8_mm takes (M, N, K) under `config` (default: choose_config)."""
     cfg = config or default_config(m, n, k)
@@ -193,6 +200,9 @@ def w8a8_mm(
         raise ValueError(f"cannot multiply {tuple(a_q.shape)} by {tuple(b_q.shape)}")
     if not (a_q.is_cuda and b_q.is_cuda):
         raise NotSupported("operands must be on a HIP device")
+    # Every pointer the kernel reads must live on the launching device: a host scale or a
+    # tensor on another GPU would be dereferenced as a device address.
+    same_device(a_q.device, b_q=b_q, scale_a=scale_a, scale_b=scale_b, bias=bias)
     m, k = a_q.shape
     n = b_q.shape[1]
     cfg = config or choose_config(m, n, k)

@@ -1,29 +1,49 @@
-"""Linear-layer shapes, as (layers, K, N) for C[M, N] = A[M, K] @ W[N, K]^T.
+"""The int8 linears of the benchmarked models, as (name, K, N) for C[M, N] = A[M, K] @ W[N, K]^T.
 
-The model dimensions are public model facts; the table is kept identical to the
-reference's int8_linear/shapes.py (AshrithaG/int8-linear, 3-27) so that shape names agree.
+Each table is derived from the model's published dimensions (hidden size, MLP width,
+attention heads and head size), either with every projection separate, as the checkpoint
+stores them, or merged the way vLLM runs them (q, k, v in one qkv_proj; gate with up).  The
+keys and names are the ones the reference's benchmarks use (AshrithaG/int8-linear
+int8_linear/shapes.py), so a shape named there means the same matrix here.
 """
 
+from __future__ import annotations
+
+from typing import NamedTuple
+
+
+class ModelDims(NamedTuple):
+    hidden: int
+    intermediate: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+
+
+QWEN3_1_7B = ModelDims(hidden=2048, intermediate=6144, q_heads=16, kv_heads=8, head_dim=128)
+LLAMA_3_8B = ModelDims(hidden=4096, intermediate=14336, q_heads=32, kv_heads=8, head_dim=128)
+
+
+def separate_linears(d: ModelDims) -> list[tuple[str, int, int]]:
+    """Distinct (K, N) of the unmerged projections; projections of one shape share a row."""
+    q, kv = d.q_heads * d.head_dim, d.kv_heads * d.head_dim
+    return [("q_proj, o_proj", d.hidden, q),
+            ("k_proj, v_proj", d.hidden, kv),
+            ("gate_proj, up_proj", d.hidden, d.intermediate),
+            ("down_proj", d.intermediate, d.hidden)]
+
+
+def merged_linears(d: ModelDims) -> list[tuple[str, int, int]]:
+    """The four GEMMs of a decoder layer as vLLM executes them at tensor parallelism 1."""
+    q, kv = d.q_heads * d.head_dim, d.kv_heads * d.head_dim
+    return [("qkv_proj", d.hidden, q + 2 * kv),
+            ("o_proj", q, d.hidden),
+            ("gate_up_proj", d.hidden, 2 * d.intermediate),
+            ("down_proj", d.intermediate, d.hidden)]
+
+
 SHAPES = {
-    # Qwen3-1.7B: hidden 2048, intermediate 6144, 16 query and 8 KV heads of 128.
-    "qwen3-1.7b": [
-        ("q_proj, o_proj", 2048, 2048),
-        ("k_proj, v_proj", 2048, 1024),
-        ("gate_proj, up_proj", 2048, 6144),
-        ("down_proj", 6144, 2048),
-    ],
-    # What vLLM runs for Qwen3-1.7B: q, k, v merged into one projection, gate with up.
-    "qwen3-1.7b-vllm": [
-        ("qkv_proj", 2048, 4096),
-        ("o_proj", 2048, 2048),
-        ("gate_up_proj", 2048, 12288),
-        ("down_proj", 6144, 2048),
-    ],
-    # Llama-3-8B at TP1, QKV and gate/up merged as vLLM runs them.
-    "llama-3-8b": [
-        ("qkv_proj", 4096, 6144),
-        ("o_proj", 4096, 4096),
-        ("gate_up_proj", 4096, 28672),
-        ("down_proj", 14336, 4096),
-    ],
+    "qwen3-1.7b": separate_linears(QWEN3_1_7B),
+    "qwen3-1.7b-vllm": merged_linears(QWEN3_1_7B),
+    "llama-3-8b": merged_linears(LLAMA_3_8B),
 }

@@ -89,8 +89,9 @@ class DecoderStandIn:
         w, ws = layer[name]
         return w8a8_mm(q, w.t(), s, ws, torch.bfloat16, config=self.configs.get(name))
 
-    def forward(self) -> torch.Tensor:
-        """One step through every layer; returns the last down_proj output [m, HIDDEN]."""
+    def forward(self, with_residual: bool = False):
+        """One step through every layer; returns the last down_proj output [m, HIDDEN] (and
+        the residual stream entering the last layer's MLP norm, with_residual=True)."""
         fused_o = self.fused_o
         res = self.x
         q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
@@ -109,7 +110,7 @@ class DecoderStandIn:
             gu = self.mm(layer, "gate_up_proj", q, s)
             q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)
             h = self.mm(layer, "down_proj", q, s)
-        return h
+        return (h, res) if with_residual else h
 
 
 def per_layer_us(stack: DecoderStandIn, windows: int = 5, min_window_ms: float = 20.0) -> float:

@@ -387,31 +387,122 @@ def matvec(w: np.ndarray, v: np.ndarray) -> np.ndarray:
     return np.concatenate([w[i:i + 2048].astype(np.int64) @ v for i in range(0, w.shape[0], 2048)])
 
 
-# Llama-3-8B shapes at prefill M, full size.
+# Llama-3-8B shapes at prefill M, full size, on BASELINE's operands
+# (x ~ N(0,1), W ~ N(0,0.02), bias ~ N(0,0.01), each quantized per row as the reference's
+# bench/bench_linear.py:146-167 does).
+def _baseline_weight(k, n, seed):
+    """W ~ N(0, 0.02) [N, K] and bias ~ N(0, 0.01) [N] in bf16, quantized per output channel."""
+    from int8_linear.operands import quant_rows
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn((n,), generator=g) * 0.01).to(torch.bfloat16)
+    w_q, w_s = quant_rows(w)
+    return w_q, w_s, bias
+
+
+def _baseline_acts(m, k, seed):
+    from int8_linear.operands import quant_rows
+    g = torch.Generator().manual_seed(seed)
+    return quant_rows(torch.randn((m, k), generator=g).to(torch.bfloat16))
+
+
+def _sample_rows(m, rng, tile=256, count=32):
+    """The first and last row of the first, second and last row tiles (and of the middle
+    one), row M-1, then random rows up to `count`."""
+    edges = {0, tile - 1, tile, 2 * tile - 1, m // 2 - 1, m // 2, m - tile, m - 1}
+    rows = {r for r in edges if 0 <= r < m}
+    while len(rows) < count:
+        rows.add(int(rng.integers(m)))
+    return np.array(sorted(rows))
+
+
 @pytest.mark.parametrize("shape", SHAPES["llama-3-8b"], ids=lambda s: s[0])
 def test_prefill_full_size_checksums_and_rows(shape):
+    """Exact int32 row and column checksums of the whole product, then 32 rows per M (tile
+    edges included) compared bit for bit in int32 and, with bias, in bf16."""
     _, k, n = shape
     rng = np.random.default_rng(k + n)
-    w = ints((n, k), k * 7 + n)
-    w_np = np_(w)
+    w_q, w_s, bias = _baseline_weight(k, n, k * 7 + n)
+    w_np = np_(w_q)
     wsum_k = w_np.sum(axis=0, dtype=np.int64)     # [K]: sum over n of W[n, k]
+    w, ws, bias_d = w_q.cuda(), w_s.cuda(), bias.cuda()
     one = torch.ones(1, device="cuda")
     for m in (512, 1024, 2048, 4096):
-        say(f"prefill {shape[0]} m={m} k={k} n={n}")
-        a = ints((m, k), m + k)
-        a_np = np_(a).astype(np.int64)
+        say(f"prefill {shape[0]} m={m} k={k} n={n} (BASELINE operands, bias)")
+        a_q, a_s = _baseline_acts(m, k, m + k)
+        a, sa = a_q.cuda(), a_s.cuda()
+        a_np = np_(a_q).astype(np.int64)
         got = w8a8_mm(a, w.t(), one, one, raw=True)
         # row checksums: sum_n C[m,n] = A[m,:] . (sum_n W[n,:]); column checksums likewise
         assert np.array_equal(np_(got.sum(dim=1, dtype=torch.int64)), a_np @ wsum_k)
         assert np.array_equal(np_(got.sum(dim=0, dtype=torch.int64)), matvec(w_np, a_np.sum(axis=0)))
-        rows = np.sort(rng.choice(m, 6, replace=False))
-        rows = np.concatenate([rows, [0, m - 1]])
-        got_rows = np_(got[torch.from_numpy(rows).cuda()])
-        assert np.array_equal(got_rows, o.gemm_i32(np_(a)[rows], np_(w)))
-        # scaled path, same rows against the oracle epilogue
-        sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
-        sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
-        out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16)
-        ref = o.epilogue(got_rows, np_(sa)[rows], np_(sb), None, o.NONE, o.BF16)
-        assert np.array_equal(bits(out[torch.from_numpy(rows).cuda()]), ref)
+        rows = _sample_rows(m, rng)
+        idx = torch.from_numpy(rows).cuda()
+        acc = o.gemm_i32(np_(a_q)[rows], w_np)
+        assert np.array_equal(np_(got[idx]), acc)
+        out = w8a8_mm(a, w.t(), sa, ws, torch.bfloat16, bias_d)
+        ref = o.epilogue(acc, np_(a_s)[rows], np_(w_s), bits(bias), o.BF16, o.BF16)
+        assert np.array_equal(bits(out[idx]), ref)
+        out = w8a8_mm(a, w.t(), sa, ws, torch.bfloat16)
+        ref = o.epilogue(acc, np_(a_s)[rows], np_(w_s), None, o.NONE, o.BF16)
+        assert np.array_equal(bits(out[idx]), ref)
         del got, out
+
+
+# The prefill tiles' epilogue in every output dtype, bias dtype and scale shape (the decode
+# tiles take these at M = 13 and 37 in test_scaled_output_matches_oracle_and_float64): one
+# tile of each prefill schedule (overlapped ring, ring, register-staged) and a 192-wide one.
+PREFILL_EPILOGUE_TILES = [Config(128, 128, 128, 4, 12, 8), Config(256, 256, 64, 8, 12, 4),
+                          Config(256, 192, 64, 4, 12, 4), Config(256, 256, 64, 8, 3, 8),
+                          Config(128, 128, 64, 4, 2, 8)]
+
+
+@pytest.mark.parametrize("config", PREFILL_EPILOGUE_TILES, ids=lambda c: c.name.replace(" ", "_"))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_prefill_epilogue_every_dtype_bias_and_scale(config, dtype):
+    m, k, n = 300, 2048, 1536
+    a, w = ints((m, k), 31), ints((n, k), 32)
+    g = torch.Generator().manual_seed(33)
+    for per_row, per_col in ((True, True), (True, False), (False, True)):
+        sa = (torch.rand((m, 1) if per_row else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+        sb = (torch.rand((n, 1) if per_col else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+        for bias_dtype in (None, torch.bfloat16, torch.float16, torch.float32):
+            say(f"prefill epilogue {config.name} {dtype} row={per_row} col={per_col} "
+                f"bias={bias_dtype}")
+            bias = torch.randn(n, generator=g).to(bias_dtype).cuda() if bias_dtype else None
+            got = w8a8_mm(a, w.t(), sa, sb, dtype, bias, config=config)
+            assert got.dtype == dtype
+            assert np.array_equal(as_np(got), oracle_out(a, w, sa, sb, bias, dtype)), \
+                (per_row, per_col, bias_dtype)
+
+
+def test_long_prefill_offsets_pass_two_to_the_31():
+    """M * K > 2^31 (M = 150000, K = 14336, Llama-3-8B down_proj): the reference indexes A
+    with int64 for this case (int8_linear/kernel.py:85-86).  Rows on both sides of
+    m * K = 2^31 and the last row tile are compared exactly with the oracle, in int32 and in
+    bf16 with bias; the column checksums cover every row of the product."""
+    m, k, n = 150_000, 14336, 4096
+    assert m * k > 2 ** 31
+    say(f"long prefill m={m} k={k} n={n} (M*K = {m * k})")
+    w_q, w_s, bias = _baseline_weight(k, n, 77)
+    w_np = np_(w_q)
+    w, ws, bias_d = w_q.cuda(), w_s.cuda(), bias.cuda()
+    g = torch.Generator(device="cuda").manual_seed(78)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8, device="cuda")
+    sa = torch.rand((m, 1), generator=g, device="cuda") * 1e-2 + 1e-3
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, w.t(), one, one, raw=True)
+    edge = 2 ** 31 // k
+    rows = np.array(sorted({0, 1, edge - 1, edge, edge + 1, m - 257, m - 256, m - 2, m - 1,
+                            m // 2}))
+    idx = torch.from_numpy(rows).cuda()
+    a_rows = np_(a[idx])
+    acc = o.gemm_i32(a_rows, w_np)
+    assert np.array_equal(np_(got[idx]), acc)
+    # column checksums: sum_m C[m, n] = (sum_m A[m, :]) . W[n, :], exact in int64
+    a_colsum = np_(a.sum(dim=0, dtype=torch.int64))
+    assert np.array_equal(np_(got.sum(dim=0, dtype=torch.int64)), matvec(w_np, a_colsum))
+    del got
+    out = w8a8_mm(a, w.t(), sa, ws, torch.bfloat16, bias_d)
+    ref = o.epilogue(acc, np_(sa)[rows], np_(w_s), bits(bias), o.BF16, o.BF16)
+    assert np.array_equal(bits(out[idx]), ref)

@@ -411,3 +411,101 @@ def test_oracle_reproduces_golden_quantizer_fixtures():
     assert np.array_equal(q, f["q_plain"]) and np.array_equal(s, f["s_plain"])
     assert f["q_plain"][2, :8].tolist() == [127, 0, 2, 2, 0, -2, -2, 126]
     assert f["s_plain"][1, 0] == 0 and not f["q_plain"][1].any()
+
+
+# ------------------------------------------------------------------ BASELINE config 2 against
+# the reference's restatement (tests/test_fused_quant.py:26-51), at full size.  The oracle and
+# the GPU kernels agree bit for bit (tests/test_quant_gpu.py), so these counts are the GPU's.
+CONFIG2_M = [1, 16, 128, 1024, 4096]
+
+
+def _config2_norm_inputs(m):
+    return randn_bf16((m, 2048), 10 + m), randn_bf16((m, 2048), 20 + m), \
+        randn_bf16((2048,), 98, 0.1) + 1.0
+
+
+def test_restatement_divides_by_a_reciprocal_product():
+    """torch evaluates `127.0 / t` as reciprocal(t) * 127: bit for bit equal to that product,
+    and not always the IEEE quotient.  This is why the restatement as written and the
+    reference kernel's IEEE division (fused_quant.py:45-47) can part by one code."""
+    rng = np.random.default_rng(5)
+    t = torch.from_numpy((np.abs(rng.standard_normal(1 << 16)) * 4 + 1e-3).astype(np.float32))
+    as_written = (127.0 / t).numpy()
+    assert np.array_equal(as_written, (t.reciprocal() * 127.0).numpy())
+    ieee = np.float32(127.0) / t.numpy()
+    assert np.array_equal((torch.full_like(t, 127.0) / t).numpy(), ieee)
+    assert 0 < np.count_nonzero(as_written != ieee) < t.numel() // 2
+
+
+@pytest.mark.parametrize("m", CONFIG2_M)
+def test_config2_restatement_made_canonical_is_the_oracle(m):
+    """With IEEE division, float64 variance and a correctly rounded rsqrt substituted, the
+    reference's restatement gives the oracle's codes and scales exactly, for both fused
+    quantizers, with and without the residual, SiLU rounded or not."""
+    import restated as rs
+    x, r, w = _config2_norm_inputs(m)
+    for res in (r, None):
+        q, s, _ = o.add_rmsnorm_quant(bf16_to_bits(x), None if res is None else bf16_to_bits(res),
+                                      bf16_to_bits(w), EPS)
+        q0, s0, _ = rs.norm(x, res, w, "ieee", canonical_var=True, canonical_rsqrt=True)
+        assert rs.differences(q, s, q0, s0) == (0, 0, 0)
+    gu = randn_bf16((m, 12288), 30 + m)
+    for round_silu in (True, False):
+        q, s = o.silu_mul_quant(bf16_to_bits(gu), round_silu=round_silu)
+        q0, s0 = rs.silu(gu, round_silu, "ieee")
+        assert rs.differences(q, s, q0, s0) == (0, 0, 0)
+
+
+@pytest.mark.parametrize("m", CONFIG2_M)
+def test_config2_restatement_with_ieee_division(m):
+    """The restatement with the IEEE division it describes (torch's float32 variance, rsqrt and
+    exp kept): scales identical, SiLU codes identical, add+RMSNorm codes off by one in at most
+    4 of M x 2048 (measured: 0-3, from the float32 variance and rsqrt roundings)."""
+    import restated as rs
+    x, r, w = _config2_norm_inputs(m)
+    for res in (r, None):
+        q, s, _ = o.add_rmsnorm_quant(bf16_to_bits(x), None if res is None else bf16_to_bits(res),
+                                      bf16_to_bits(w), EPS)
+        n, dmax, sdiff = rs.differences(q, s, *rs.norm(x, res, w, "ieee")[:2])
+        assert sdiff == 0 and dmax <= 1 and n <= 4, (m, res is not None, n)
+    gu = randn_bf16((m, 12288), 30 + m)
+    for round_silu in (True, False):
+        q, s = o.silu_mul_quant(bf16_to_bits(gu), round_silu=round_silu)
+        assert rs.differences(q, s, *rs.silu(gu, round_silu, "ieee")) == (0, 0, 0)
+
+
+# codes that differ from the restatement as written, per M: norm with/without residual, SiLU
+# rounded/not (measured with this oracle, which the GPU matches bit for bit)
+AS_WRITTEN = {1: (0, 0, 0, 0), 16: (5, 10, 2, 4), 128: (36, 31, 16, 14),
+              1024: (278, 304, 92, 97), 4096: (1131, 1162, 377, 348)}
+
+
+@pytest.mark.parametrize("m", CONFIG2_M)
+def test_config2_restatement_as_written(m):
+    """Against the restatement exactly as the reference wrote it: scales identical, codes off
+    by at most one in at most 0.015% of elements (16 allowed in small tensors), every such code
+    explained by the reciprocal-product division (the oracle's precise_div=False mode, which
+    multiplies by the IEEE reciprocal, gives the restatement's SiLU codes exactly)."""
+    import restated as rs
+    x, r, w = _config2_norm_inputs(m)
+    counts = []
+    for res in (r, None):
+        xb, rb = bf16_to_bits(x), None if res is None else bf16_to_bits(res)
+        q, s, _ = o.add_rmsnorm_quant(xb, rb, bf16_to_bits(w), EPS)
+        q0, s0, _ = rs.norm(x, res, w)
+        n, dmax, sdiff = rs.differences(q, s, q0, s0)
+        assert sdiff == 0 and dmax <= 1 and n <= max(16, 1.5e-4 * q.size)
+        counts.append(n)
+    gu = randn_bf16((m, 12288), 30 + m)
+    for round_silu in (True, False):
+        q, s = o.silu_mul_quant(bf16_to_bits(gu), round_silu=round_silu)
+        q0, s0 = rs.silu(gu, round_silu)
+        n, dmax, sdiff = rs.differences(q, s, q0, s0)
+        assert sdiff == 0 and dmax <= 1 and n <= max(16, 1.5e-4 * q.size)
+        counts.append(n)
+        # (its scales are absmax * (1/127), so only the codes are compared)
+        qr, _ = o.silu_mul_quant(bf16_to_bits(gu), round_silu=round_silu, precise_div=False)
+        assert np.array_equal(qr, q0.numpy())
+    # the recorded counts, with slack for another CPU's torch kernels
+    for got, want in zip(counts, AS_WRITTEN[m]):
+        assert abs(got - want) <= max(4, want // 20), (m, counts)

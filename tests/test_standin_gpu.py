@@ -22,9 +22,11 @@ from oracle import oracle as o
 pytestmark = pytest.mark.gpu
 
 
-def oracle_step(stack: DecoderStandIn) -> tuple[np.ndarray, np.ndarray]:
-    """The same chain on the CPU oracle: (last h bits, residual bits)."""
-    x = bits(stack.x)
+def oracle_step(stack: DecoderStandIn, rows=None) -> tuple[np.ndarray, np.ndarray]:
+    """The same chain on the CPU oracle: (last h bits, residual bits).  Every op of the chain
+    works on each token row alone, so with `rows` given the oracle runs on those token rows
+    only and its result is exactly those rows of the full step."""
+    x = bits(stack.x) if rows is None else bits(stack.x)[rows]
     gamma = bits(stack.norm)
     precise, round_silu = fq.PRECISE_DIV, fq.ROUND_SILU
 
@@ -48,17 +50,38 @@ def oracle_step(stack: DecoderStandIn) -> tuple[np.ndarray, np.ndarray]:
     return h, res
 
 
-@pytest.mark.parametrize("m,layers", [(1, 3), (8, 3), (17, 2), (128, 2), (300, 1)])
+@pytest.mark.parametrize("m,layers", [(1, 3), (8, 3), (17, 2), (32, 3), (128, 2), (300, 1)])
 @pytest.mark.parametrize("round_silu", [False, True])
 def test_standin_matches_oracle_bit_for_bit(m, layers, round_silu, monkeypatch):
     say(f"standin m={m} layers={layers} round_silu={round_silu}")
     monkeypatch.setattr(fq, "ROUND_SILU", round_silu)
     stack = DecoderStandIn(m, layers=layers, seed=m)
-    h = stack.forward()
+    h, res = stack.forward(with_residual=True)
     torch.cuda.synchronize()
-    h0, _ = oracle_step(stack)
+    h0, r0 = oracle_step(stack)
     assert h.shape == (m, 2048) and h.dtype == torch.bfloat16
     assert np.array_equal(bits(h), h0)
+    assert np.array_equal(bits(res), r0)
+
+
+@pytest.mark.parametrize("round_silu", [False, True])
+def test_prefill_step_matches_oracle_on_sampled_rows(round_silu, monkeypatch):
+    """The 4096-token step the benchmark times (prefill regime: every GEMM on the macro-tile
+    schedules), two layers, compared with the oracle on the first, last and tile-edge token
+    rows and six random ones: final output and residual stream, bit for bit."""
+    m = 4096
+    say(f"standin prefill m={m} layers=2 round_silu={round_silu}, sampled rows")
+    monkeypatch.setattr(fq, "ROUND_SILU", round_silu)
+    stack = DecoderStandIn(m, layers=2, seed=4096)
+    h, res = stack.forward(with_residual=True)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7 + round_silu)
+    rows = np.unique(np.concatenate([[0, 1, 127, 128, 255, 256, 2047, 4095],
+                                     rng.choice(m, 6, replace=False)]))
+    h0, r0 = oracle_step(stack, rows)
+    idx = torch.from_numpy(rows).cuda()
+    assert np.array_equal(bits(h[idx]), h0)
+    assert np.array_equal(bits(res[idx]), r0)
 
 
 def test_standin_graph_replay_equals_eager():

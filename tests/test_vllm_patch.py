@@ -5,6 +5,7 @@ plain classes and monkeypatches stand in for it, as in the reference."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -87,12 +88,143 @@ def test_declined_shapes_raise_without_a_replaced_kernel(monkeypatch):
         vllm_patch.scaled_mm(a, w, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
 
 
+class _Int8Kernel:
+    """Stands in for one of vLLM's int8 linear kernels: its own apply_weights quantizes the
+    bf16 input per token and calls the matmul, as vLLM's does (scaled_int8_quant then
+    triton_scaled_mm); _get_layer_params hands out the layer's int8 weight and scales."""
+
+    def _get_layer_params(self, layer):
+        return layer.w_qt, layer.w_s, None, None, None
+
+    def apply_weights(self, layer, x, bias=None):
+        from int8_linear import fused_quant as fq
+        q, s = fq.quant_per_token(x)
+        return vllm_patch.scaled_mm(q, layer.w_qt, scale_a=s, scale_b=layer.w_s,
+                                    out_dtype=x.dtype, bias=bias)
+
+
+class _Linear:
+    """vLLM's linear module surface: forward returns (output, output_bias)."""
+
+    kernel = _Int8Kernel()
+
+    def __init__(self, w_q, w_s):
+        self.w_q, self.w_qt, self.w_s = w_q, w_q.t(), w_s
+
+    def __call__(self, x):
+        return self.kernel.apply_weights(self, x, None), None
+
+
+class _Norm:
+    def __init__(self, weight, eps):
+        self.weight, self.variance_epsilon = weight, eps
+
+
+class _Attention:
+    """Attention left out as in the decoder stand-in: the q columns of qkv_proj's output
+    feed o_proj, which quantizes its own input (no kernel before it to fuse into)."""
+
+    def __init__(self, qkv, o):
+        self.qkv_proj, self.o_proj = qkv, o
+
+    def __call__(self, positions, hidden_states):
+        qkv = self.qkv_proj(hidden_states)[0]
+        return self.o_proj(qkv[:, :2048])[0]
+
+
+class _MLP:
+    def __init__(self, gate_up, down):
+        self.gate_up_proj, self.down_proj = gate_up, down
+
+    def __call__(self, x):
+        return vfp._mlp_forward(self, x)
+
+
+class _DecoderLayer:
+    def __init__(self, gen):
+        def linear(k, n):
+            w = torch.randint(-127, 128, (n, k), generator=gen, dtype=torch.int8)
+            s = torch.rand((n, 1), generator=gen) * 1e-3 + 1e-4
+            return _Linear(w.cuda(), s.cuda())
+
+        one = torch.ones(2048, dtype=torch.bfloat16, device="cuda")
+        self.input_layernorm = _Norm(one, 1e-6)
+        self.post_attention_layernorm = _Norm(one, 1e-6)
+        self.self_attn = _Attention(linear(2048, 4096), linear(2048, 2048))
+        self.mlp = _MLP(linear(2048, 12288), linear(6144, 2048))
+
+    def forward(self, positions, hidden_states, residual):
+        return vfp._decoder_forward(self, positions, hidden_states, residual)
+
+
+def _oracle_layers(layers, x_bits):
+    """The routed layers' arithmetic on the CPU oracle: (hidden bits, residual bits)."""
+    from int8_linear import fused_quant as fq
+    from oracle import oracle as o
+    from helpers import bits, np_
+
+    precise = fq.PRECISE_DIV
+
+    def mm(lin, q, s):
+        return o.w8a8_mm(q, np_(lin.w_q), s, np_(lin.w_s), out_dt=o.BF16)
+
+    h, res = x_bits, None
+    for layer in layers:
+        gamma = bits(layer.input_layernorm.weight)
+        if res is None:
+            q, s, _ = o.add_rmsnorm_quant(h, None, gamma, 1e-6, precise_div=precise)
+            res = h
+        else:
+            q, s, res = o.add_rmsnorm_quant(h, res, gamma, 1e-6, precise_div=precise)
+        qkv = mm(layer.self_attn.qkv_proj, q, s)
+        q, s = o.quant_per_token(qkv[:, :2048], precise_div=precise)
+        h = mm(layer.self_attn.o_proj, q, s)
+        q, s, res = o.add_rmsnorm_quant(h, res, bits(layer.post_attention_layernorm.weight),
+                                        1e-6, precise_div=precise)
+        gu = mm(layer.mlp.gate_up_proj, q, s)
+        q, s = o.silu_mul_quant(gu, round_silu=fq.ROUND_SILU, precise_div=precise)
+        h = mm(layer.mlp.down_proj, q, s)
+    return h, res
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 8, 32])
+@pytest.mark.parametrize("round_silu", [False, True])
+def test_routed_decoder_layers_match_the_oracle_chain(m, round_silu, monkeypatch):
+    """Two Qwen3 decoder layers run through the routing (the norms and SiLU-and-mul hand
+    qkv_proj, gate_up_proj and down_proj a PreQuant; the wrapped apply_weights sends it to
+    scaled_mm) equal the oracle's chain of add_rmsnorm_quant, w8a8_mm, quant_per_token and
+    silu_mul_quant bit for bit: final hidden state and residual stream."""
+    from int8_linear import fused_quant as fq
+    from helpers import bits
+    say(f"routed decoder layers m={m} round_silu={round_silu}")
+    monkeypatch.setattr(fq, "ROUND_SILU", round_silu)
+    monkeypatch.setitem(vfp._ROUTES, _Int8Kernel, _Int8Kernel.apply_weights)
+    monkeypatch.setattr(_Int8Kernel, "apply_weights", _Int8Kernel.apply_weights)
+    vfp._wrap_apply(_Int8Kernel, lambda a, w, sa, sb, dt, b: vllm_patch.scaled_mm(
+        a, w, scale_a=sa, scale_b=sb, out_dtype=dt, bias=b))
+    gen = torch.Generator().manual_seed(100 + m)
+    layers = [_DecoderLayer(gen) for _ in range(2)]
+    x = torch.randn((m, 2048), generator=gen).to(torch.bfloat16).cuda()
+    before = vfp.PREQUANT_CALLS
+    h, res = x, None
+    for layer in layers:
+        h, res = layer.forward(None, h, res)
+    torch.cuda.synchronize()
+    assert vfp.PREQUANT_CALLS == before + 3 * len(layers)     # qkv, gate_up, down per layer
+    h0, r0 = _oracle_layers(layers, bits(x))
+    assert np.array_equal(bits(h), h0)
+    assert np.array_equal(bits(res), r0)
+
+
 @pytest.mark.gpu
 def test_prequant_feeds_the_kernel_end_to_end():
-    """add_rmsnorm_quant -> PreQuant -> wrapped apply_weights -> scaled_mm, as the patched
-    Qwen3 layer runs it, equals quantizing separately and calling the kernel."""
+    """add_rmsnorm_quant -> PreQuant -> wrapped apply_weights -> scaled_mm equals the
+    oracle's add_rmsnorm_quant followed by its w8a8_mm, bit for bit."""
     from int8_linear import fused_quant as fq
-    say("prequant end to end")
+    from oracle import oracle as o
+    from helpers import bits, np_
+    say("prequant end to end vs oracle")
 
     class Kernel:
         def __init__(self, w_q, w_s):
@@ -107,14 +239,20 @@ def test_prequant_feeds_the_kernel_end_to_end():
     vfp._wrap_apply(Kernel, lambda a, w, sa, sb, dt, b: vllm_patch.scaled_mm(
         a, w, scale_a=sa, scale_b=sb, out_dtype=dt, bias=b))
     g = torch.Generator().manual_seed(3)
-    x = torch.randn((8, 2048), generator=g).to(torch.bfloat16).cuda()
-    r = torch.randn((8, 2048), generator=g).to(torch.bfloat16).cuda()
-    gamma = torch.ones(2048, dtype=torch.bfloat16, device="cuda")
-    w_q = ints((4096, 2048), 5).t()
-    w_s = torch.rand((4096, 1), device="cuda") * 1e-3 + 1e-4
-    q, s, res = fq.add_rmsnorm_quant_op(x, r, gamma, 1e-6)
-    got = Kernel(w_q, w_s).apply_weights(None, vfp.PreQuant(q, s, torch.bfloat16))
-    assert torch.equal(got, w8a8_mm(q, w_q, s, w_s, torch.bfloat16))
+    x = torch.randn((8, 2048), generator=g).to(torch.bfloat16)
+    r = torch.randn((8, 2048), generator=g).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(2048, generator=g)).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (4096, 2048), generator=g, dtype=torch.int8)
+    w_s = torch.rand((4096, 1), generator=g) * 1e-3 + 1e-4
+    bias = (torch.randn(4096, generator=g) * 0.01).to(torch.bfloat16)
+    q, s, res = fq.add_rmsnorm_quant_op(x.cuda(), r.cuda(), gamma.cuda(), 1e-6)
+    got = Kernel(w.cuda().t(), w_s.cuda()).apply_weights(
+        None, vfp.PreQuant(q, s, torch.bfloat16), bias.cuda())
+    q0, s0, r0 = o.add_rmsnorm_quant(bits(x), bits(r), bits(gamma), 1e-6,
+                                     precise_div=fq.PRECISE_DIV)
+    want = o.w8a8_mm(q0, np_(w), s0, np_(w_s), bits(bias), o.BF16, o.BF16)
+    assert np.array_equal(bits(got), want)
+    assert np.array_equal(bits(res), r0)
 
 
 # ------------------------------------------------------------------ CPU (routing only)
@@ -200,3 +338,95 @@ def test_patch_vllm_rebinds_the_module_name(monkeypatch):
     assert vllm_patch._vllm_triton_scaled_mm is original
     vllm_patch.patch_vllm()            # idempotent: the saved original is kept
     assert vllm_patch._vllm_triton_scaled_mm is original
+
+
+def _fake_vllm(monkeypatch):
+    """Minimal vllm modules with the classes patch_vllm routes (no vLLM is installed)."""
+    import sys
+    import types
+
+    class Kernel:
+        def apply_weights(self, layer, x, bias=None):
+            return "original"
+
+    class Triton(Kernel):
+        pass
+
+    class Cutlass(Kernel):
+        def apply_weights(self, layer, x, bias=None):
+            return "cutlass original"
+
+    class Decoder:
+        def forward(self, *a):
+            return "decoder original"
+
+    class MLP:
+        def forward(self, *a):
+            return "mlp original"
+
+    tree = {"vllm": {}, "vllm._custom_ops": {"cutlass_scaled_mm": lambda *a, **k: "cutlass"},
+            "vllm.model_executor": {}, "vllm.model_executor.kernels": {},
+            "vllm.model_executor.kernels.linear": {},
+            "vllm.model_executor.kernels.linear.scaled_mm": {},
+            "vllm.model_executor.kernels.linear.scaled_mm.triton": {
+                "TritonInt8ScaledMMLinearKernel": Triton,
+                "triton_scaled_mm": lambda *a, **k: "triton"},
+            "vllm.model_executor.kernels.linear.scaled_mm.cutlass": {
+                "CutlassInt8ScaledMMLinearKernel": Cutlass},
+            "vllm.model_executor.models": {},
+            "vllm.model_executor.models.qwen3": {"Qwen3DecoderLayer": Decoder},
+            "vllm.model_executor.models.qwen2": {"Qwen2MLP": MLP}}
+    mods = {}
+    for name, attrs in tree.items():
+        mod = types.ModuleType(name)
+        for k, v in attrs.items():
+            setattr(mod, k, v)
+        mods[name] = mod
+        monkeypatch.setitem(sys.modules, name, mod)
+    for name, mod in mods.items():
+        if "." in name:
+            parent, child = name.rsplit(".", 1)
+            setattr(mods[parent], child, mod)
+    return Triton, Cutlass, Decoder, MLP
+
+
+def test_fuse_patch_is_idempotent_and_undone(monkeypatch):
+    from int8_linear import fused_quant as fq
+    triton_k, cutlass_k, decoder, mlp = _fake_vllm(monkeypatch)
+    monkeypatch.setattr(fq, "PRECISE_DIV", fq.PRECISE_DIV)
+    monkeypatch.setattr(fq, "ROUND_SILU", fq.ROUND_SILU)
+    originals = (triton_k.apply_weights, cutlass_k.apply_weights, decoder.forward, mlp.forward)
+    vfp.patch_vllm()
+    routed = triton_k.apply_weights
+    vfp.patch_vllm()                                   # twice: the router does not nest
+    assert triton_k.apply_weights.__wrapped__ is originals[0]
+    assert cutlass_k.apply_weights.__wrapped__ is originals[1]
+    assert routed.__wrapped__ is triton_k.apply_weights.__wrapped__
+    assert decoder.forward is vfp._decoder_forward and mlp.forward is vfp._mlp_forward
+    assert triton_k().apply_weights(None, torch.zeros(1)) == "original"
+    assert cutlass_k().apply_weights(None, torch.zeros(1)) == "cutlass original"
+    vfp.unpatch_vllm()
+    assert (triton_k.apply_weights, cutlass_k.apply_weights, decoder.forward,
+            mlp.forward) == originals
+
+
+def test_prequant_reaches_the_swapped_triton_matmul(monkeypatch):
+    """The Triton route looks triton_scaled_mm up at call time, so a PreQuant reaches
+    whatever the module holds then (vllm_patch's scaled_mm once that patch is applied)."""
+    import sys
+    from int8_linear import fused_quant as fq
+    triton_k, *_ = _fake_vllm(monkeypatch)
+    monkeypatch.setattr(fq, "PRECISE_DIV", fq.PRECISE_DIV)
+    monkeypatch.setattr(fq, "ROUND_SILU", fq.ROUND_SILU)
+    vfp.patch_vllm()
+    try:
+        mod = sys.modules["vllm.model_executor.kernels.linear.scaled_mm.triton"]
+        seen = []
+        mod.triton_scaled_mm = lambda a, w, **kw: seen.append((a, w, kw)) or "swapped"
+        k = triton_k()
+        k._get_layer_params = lambda layer: ("w_q", "w_s", None, None, None)
+        assert k.apply_weights(None, vfp.PreQuant("q", "s", torch.bfloat16), "b") == "swapped"
+        assert seen == [("q", "w_q", {"scale_a": "s", "scale_b": "w_s",
+                                      "out_dtype": torch.bfloat16, "bias": "b"})]
+    finally:
+        vfp.unpatch_vllm()
