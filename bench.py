@@ -17,11 +17,14 @@ bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3
 28-layer decoder stand-in in microseconds per layer (config 4), the CPU baseline (the
 oracle's CPU restatement of the reference's path, on a bounded sample) and, beside it, the
 reference's own CPU path as torch ops (`cpu_reference_path`: torch._int_mm and an int32
-matmul with the fp32 dequant for config 0, the torch quantizers at 1024 tokens).
+matmul with the fp32 dequant for config 0, the torch quantizers at 1024 tokens), and the
+hardware floors (`floors`: empty-kernel launch, cold HBM reads, sustained int8 MFMA rate)
+measured by probe kernels the same way.
 
     python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
     python bench.py --only standin       # one extra section alone
-                                         # (quant|prefill|standin|launch|llama_decode)
+                                         # (quant|prefill|standin|launch|llama_decode|floors)
+    python bench.py --only prefill --prefill-m 4096   # config 3 at M=4096 only
 Every GPU output is checked against a float64 reference before it is timed, after the
 output buffer has been poisoned.  Prints ONE JSON line.
 """
@@ -119,19 +122,20 @@ def check_linear(out, d) -> float:
 
 class Sweep:
     """The decode sweep's operands.  Each shape has one weight (seeded as the benchmark's
-    M=16 point) held in several copies that calls rotate through; each (M, bias) point
-    has its own seeded activations and bias."""
+    M=16 point) held in enough copies of its own (>= ROTATE_BYTES per shape) that a copy is
+    read again only after at least 768 MiB of other weights; each (M, bias) point has its own
+    seeded activations and bias."""
 
     def __init__(self, shapes, ms, device):
         import torch
 
         from int8_linear.operands import operands, seed_of
-        per_set = sum(k * n for _, k, n in shapes)
-        self.copies = max(2, -(-ROTATE_BYTES // per_set))
         self.weights = {}   # (k, n) -> ([w_q copies], w_s)
+        self.copies = {}    # (k, n) -> number of copies
         for _, k, n in shapes:
             d = operands(16, k, n, seed_of(16, k, n), device=device)
-            self.weights[(k, n)] = ([d["w_q"]] + [d["w_q"].clone() for _ in range(self.copies - 1)],
+            c = self.copies[(k, n)] = max(2, -(-ROTATE_BYTES // (k * n)))
+            self.weights[(k, n)] = ([d["w_q"]] + [d["w_q"].clone() for _ in range(c - 1)],
                                     d["w_s"])
         self.points = []    # (label, m, k, n, bias, operand dict)
         for label, k, n in shapes:
@@ -148,8 +152,37 @@ class Sweep:
         import torch
         label, m, k, n, bias, d = self.points[idx]
         ws, w_s = self.weights[(k, n)]
-        return w8a8_mm(d["a_q"], ws[copy % self.copies].t(), d["a_s"], w_s, torch.bfloat16,
+        return w8a8_mm(d["a_q"], ws[copy % len(ws)].t(), d["a_s"], w_s, torch.bfloat16,
                        d["bias"])
+
+    def min_reuse_bytes(self, plan: list[list[int]]) -> int:
+        """Fewest weight bytes read between two reads of one copy when the steps of `plan`
+        replay in turn, repeatedly (the timed loop alternates them)."""
+        seq = [(self.points[i][2], self.points[i][3], c) for row in plan
+               for i, c in enumerate(row)]
+        seq = seq + seq                     # the cycle, twice: reuses across the wrap too
+        last, best, total = {}, None, 0
+        for k, n, c in seq:
+            key = (k, n, c % self.copies[(k, n)])
+            if key in last:
+                gap = total - last[key]
+                best = gap if best is None else min(best, gap)
+            total += k * n
+            last[key] = total
+        return best or 0
+
+    def step_copies(self, reps: int) -> list[list[int]]:
+        """For `reps` consecutive steps over every point, the copy each call reads: a shape's
+        calls take its copies in turn, so between two reads of one copy lie all the others."""
+        seen = {kn: 0 for kn in self.copies}
+        out = []
+        for _ in range(reps):
+            row = []
+            for _, _, k, n, _, _ in self.points:
+                row.append(seen[(k, n)])
+                seen[(k, n)] += 1
+            out.append(row)
+        return out
 
 
 TRAFFIC_PATH = ROOT / "profiles" / "traffic_config0.json"
@@ -245,13 +278,22 @@ def cpu_reference_path(seconds: float = 2.0) -> dict:
 
     from int8_linear.operands import operands, seed_of
 
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)     # pinned: every leg runs on the same thread count
+
     def per_call_us(fn) -> tuple[float, int]:
+        """Median over 5 windows of about seconds/5 each (after two warm-up calls)."""
         fn()
-        reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds or reps < 3:
-            fn()
-            reps += 1
-        return (time.perf_counter() - t0) / reps * 1e6, reps
+        fn()
+        windows, total = [], 0
+        for _ in range(5):
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < seconds / 5 or reps < 2:
+                fn()
+                reps += 1
+            windows.append((time.perf_counter() - t0) / reps * 1e6)
+            total += reps
+        return statistics.median(windows), total
 
     m, k, n = 16, 2048, 4096
     d = operands(m, k, n, seed_of(m, k, n))
@@ -288,7 +330,8 @@ def cpu_reference_path(seconds: float = 2.0) -> dict:
             "add_rmsnorm_quant": norm, "silu_mul_quant": silu}
     out = {"unit": "us per call", "threads": torch.get_num_threads(),
            "sample": f"config 0 GEMM (M=16, K=2048, N=4096) and config 2 quantizers at M={mq} "
-                     f"(H={h}, I={inter}), torch CPU ops, about {seconds:g} s a leg"}
+                     f"(H={h}, I={inter}), torch CPU ops on {threads} threads, median of 5 "
+                     f"windows, about {seconds:g} s a leg"}
     for name, fn in legs.items():
         us, reps = per_call_us(fn)
         out[name] = round(us, 2)
@@ -305,9 +348,14 @@ def main() -> int:
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
-    ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch", "llama_decode"],
+    ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch", "llama_decode",
+                                       "floors"],
                     default=None,
                     help="run one extra section alone (for profiling) and print its JSON")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="with --only: also run three 256 MiB device copies (counter scale)")
+    ap.add_argument("--prefill-m", type=int, nargs="+", default=None,
+                    help="with --only prefill: the token counts to run (default 512-4096)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
@@ -327,13 +375,17 @@ def main() -> int:
         print(json.dumps({"roofline": rf, "calibration": cal}), flush=True)
         return 0
     if args.only:
-        fn = {"quant": bench_quant, "prefill": bench_prefill, "standin": bench_standin,
-              "launch": bench_launch, "llama_decode": bench_llama_decode}[args.only]
-        print(json.dumps({args.only: fn(dev)}), flush=True)
+        fn = {"quant": bench_quant, "prefill": lambda d: bench_prefill(d, args.prefill_m),
+              "standin": bench_standin, "launch": bench_launch,
+              "llama_decode": bench_llama_decode, "floors": bench_floors}[args.only]
+        res = {args.only: fn(dev)}
+        if args.calibrate:
+            res["calibration"] = copy_calibration(dev)
+        print(json.dumps(res), flush=True)
         return 0
     shapes = SHAPES["qwen3-1.7b-vllm"]
     sw = Sweep(shapes, DECODE_M, dev)
-    log(f"sweep: {len(sw.points)} linears, {sw.copies} weight copies")
+    log(f"sweep: {len(sw.points)} linears, weight copies per shape {sorted(sw.copies.values())}")
 
     # correctness first, into poisoned outputs
     worst = 0.0
@@ -346,10 +398,13 @@ def main() -> int:
             raise SystemExit(f"FAIL: {label} M={m} bias={bias}: max rel err {err}")
     log(f"sweep checked against float64: worst rel err {worst:.3g}")
 
-    # one step = the whole sweep, each call on its own weight copy, one graph
+    # one step = the whole sweep, each call on its own weight copy, one graph (two graphs
+    # alternate, so consecutive steps read different copies too)
+    plan = sw.step_copies(2)
+
     def step_calls(rep: int):
         for i in range(len(sw.points)):
-            sw.call(i, rep * len(sw.points) + i)
+            sw.call(i, plan[rep][i])
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -387,7 +442,9 @@ def main() -> int:
         "config": {"workload": "BASELINE config 1: decode sweep, Qwen3-1.7B vLLM shapes "
                                "(qkv 2048->4096, o 2048->2048, gate_up 2048->12288, "
                                "down 6144->2048) x M{1,2,4,8,16,17,32,64,128} x bias{off,on}",
-                   "linears_per_step": n_calls, "weight_copies": sw.copies,
+                   "linears_per_step": n_calls,
+                   "weight_copies": {f"{k}x{n}": c for (k, n), c in sw.copies.items()},
+                   "min_reuse_MiB": round(sw.min_reuse_bytes(plan) / 2 ** 20, 1),
                    "sweep_GBps": round(sweep_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
     }
 
@@ -398,7 +455,7 @@ def main() -> int:
     if not args.no_extra:
         table = []
         for i, (label, m, k, n, bias, d) in enumerate(sw.points):
-            us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies, windows=3)
+            us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies[(k, n)], windows=3)
             gbs = gemm_bytes(m, k, n, bias) / (us * 1e-6) / 1e9
             table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
         result["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
@@ -407,6 +464,7 @@ def main() -> int:
         result["prefill"] = bench_prefill(dev)
         result["standin"] = bench_standin(dev)
         result["launch"] = bench_launch(dev)
+        result["floors"] = bench_floors(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
         result["cpu_reference_path"] = cpu_reference_path()
@@ -628,21 +686,33 @@ def bench_launch(dev, iters: int = 300, windows: int = 5) -> dict:
             "iters": iters, "windows": windows}
 
 
-def bench_prefill(dev) -> dict:
-    """Llama-3-8B shapes at prefill M; int8 TOP/s and MFMA fraction."""
+PREFILL_TRAFFIC_PATH = ROOT / "profiles" / "traffic_prefill_config3.json"
+
+
+def bench_prefill(dev, ms=None) -> dict:
+    """Llama-3-8B shapes at prefill M, int8 TOP/s against the 5.0 POP/s
+    dense int8 MFMA peak.  `roofline` is the dominant launch (gate_up at M=4096, the longest),
+    `per_shape` the same object for each shape at M=4096; `achieved` = 2*M*N*K ops per launch
+    / the average launch time of back-to-back launches in a HIP graph (HIP events on the
+    launch stream)."""
     import torch
 
     from int8_linear import w8a8_mm
+    from int8_linear.kernel import choose_config
     from int8_linear.operands import quant_rows
     from int8_linear.shapes import SHAPES
-    rows = []
+    ms = ms or PREFILL_M
+    traffic = {}
+    if PREFILL_TRAFFIC_PATH.exists():
+        traffic = json.loads(PREFILL_TRAFFIC_PATH.read_text()).get("shapes", {})
+    rows, per_shape = [], {}
     for label, k, n in SHAPES["llama-3-8b"]:
         g = torch.Generator().manual_seed(k + n)
         w = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16)
         w_q, w_s = quant_rows(w)
         w_q, w_s = w_q.to(dev), w_s.to(dev)
         del w
-        for m in PREFILL_M:
+        for m in ms:
             x = torch.randn((m, k), generator=g).to(torch.bfloat16)
             a_q, a_s = quant_rows(x)
             a_q, a_s = a_q.to(dev), a_s.to(dev)
@@ -652,11 +722,110 @@ def bench_prefill(dev) -> dict:
             if not err <= 1e-2:
                 raise SystemExit(f"FAIL prefill {label} M={m}: rel err {err}")
             us = graph_time_us(lambda i: w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16), 10, 3)
-            tops = 2 * m * n * k / (us * 1e-6) / 1e12
+            ops = 2 * m * n * k
+            tops = ops / (us * 1e-6) / 1e12
             rows.append([label, m, round(us, 2), round(tops, 1), round(tops / INT8_PEAK_TOPS, 3)])
             log(f"prefill {label} M={m}: {us:.1f} us {tops:.0f} TOP/s")
+            if m == max(ms):
+                cfg = choose_config(m, n, k)
+                rec = traffic.get(label, {})
+                per_shape[label] = {
+                    "bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                    "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                    "traffic": rec.get("bytes_per_launch") if rec.get("config") == cfg.name
+                    else None,
+                    "kernel": f"{schedule_of(cfg, k)}, config {cfg.name} "
+                              f"(Llama-3-8B {label}: M={m} K={k} N={n})",
+                    "ops_per_launch": ops, "avg_launch_us": round(us, 3), "launches": 10}
         del w_q, w_s
-    return {"cols": ["shape", "M", "us", "TOPs", "mfma_frac"], "rows": rows}
+    out = {"cols": ["shape", "M", "us", "TOPs", "mfma_frac"], "rows": rows,
+           "per_shape": per_shape}
+    if per_shape:
+        dominant = max(per_shape, key=lambda lbl: per_shape[lbl]["avg_launch_us"])
+        out["roofline"] = per_shape[dominant]
+    return out
+
+
+PROBES_LIB = ROOT / "int8-linear_amd" / "probes" / "libi8l_floors.so"
+
+
+def bench_floors(dev) -> dict:
+    """What the hardware gives a kernel of each regime, measured the way the kernels are
+    (back-to-back launches in a HIP graph, HIP events on the launch stream), by the probe
+    kernels of int8-linear_amd/probes/i8l_floors.hip:
+      * an empty kernel at three grid shapes (the decode GEMM's is 256 x 512 threads);
+      * a read of 8 / 12 / 24 / 120 MiB (the weights of config 0, of Qwen3 down_proj and
+        gate_up, of Llama-3-8B gate_up) rotating through >= 768 MiB of buffers so every read
+        comes from HBM, and 8 MiB hot; the best of 1, 2, 4 and 8 loads a thread;
+      * back-to-back int8 MFMAs on every SIMD: the rate sustained under load, on constant
+        operands and on random ones (toggling data costs power, and the clock follows)."""
+    import ctypes
+
+    import torch
+
+    from int8_linear import _lib
+    _lib.lib()                               # torch's HIP runtime first
+    L = ctypes.CDLL(str(PROBES_LIB))
+    L.fl_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L.fl_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                          ctypes.c_void_p]
+    L.fl_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                          ctypes.c_void_p, ctypes.c_void_p]
+
+    def stream():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def ok(rc):
+        if rc != 0:
+            raise SystemExit(f"FAIL floor probe launch: status {rc}")
+
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    empty = []
+    for blocks, threads in ((1, 64), (256, 512), (1024, 256)):
+        us = graph_time_us(lambda i: ok(L.fl_empty(blocks, threads, stream())), 200)
+        empty.append([blocks, threads, round(us, 3)])
+        log(f"floor empty kernel {blocks}x{threads}: {us:.2f} us")
+    reads = []
+    for mib, cold in ((8, True), (12, True), (24, True), (120, True), (8, False)):
+        size = mib << 20
+        copies = max(2, -(-ROTATE_BYTES // size)) if cold else 1
+        bufs = [torch.zeros(size, dtype=torch.uint8, device=dev) for _ in range(copies)]
+        per_unroll = {}
+        for unroll in (1, 2, 4, 8):
+            per_unroll[unroll] = graph_time_us(
+                lambda i: ok(L.fl_read(bufs[i % copies].data_ptr(), size, sink.data_ptr(),
+                                       unroll, stream())), 2 * copies if cold else 50)
+        best = min(per_unroll, key=per_unroll.get)
+        us = per_unroll[best]
+        gbs = size / (us * 1e-6) / 1e9
+        reads.append([mib, "cold" if cold else "hot", round(us, 3), round(gbs, 1),
+                      round(gbs / HBM_PEAK_GBS, 3), best,
+                      {u: round(t, 3) for u, t in per_unroll.items()}])
+        log(f"floor read {mib} MiB {'cold' if cold else 'hot'}: {us:.2f} us {gbs:.0f} GB/s "
+            f"(loads a thread {best}; all: {per_unroll})")
+        del bufs
+    mfma = []
+    props = torch.cuda.get_device_properties(dev)
+    blocks, iters = 8 * props.multi_processor_count, 1000
+    rnd = torch.randint(-128, 128, (4096,), dtype=torch.int8,
+                        generator=torch.Generator().manual_seed(0)).to(dev)
+    for kind, ops_each in ((32, 65536), (16, 32768)):
+        for operands, data in (("constant", None), ("random", rnd.data_ptr())):
+            us = graph_time_us(lambda i: ok(L.fl_mfma(kind, blocks, iters, data,
+                                                      sink.data_ptr(), stream())), 5)
+            tops = blocks * 4 * iters * 4 * ops_each / (us * 1e-6) / 1e12
+            name = "v_mfma_i32_32x32x32_i8" if kind == 32 else "v_mfma_i32_16x16x64_i8"
+            mfma.append([name, operands, round(us, 1), round(tops, 1),
+                         round(tops / INT8_PEAK_TOPS, 3)])
+            log(f"floor {name} {operands} operands: {tops:.0f} TOP/s")
+    torch.cuda.empty_cache()
+    return {"empty_kernel": {"cols": ["blocks", "threads", "us"], "rows": empty},
+            "read": {"cols": ["MiB", "cache", "us", "GBps", "hbm_frac", "loads_per_thread",
+                              "us_by_loads_per_thread"], "rows": reads},
+            "mfma": {"cols": ["instruction", "operands", "us", "TOPs", "frac_of_5000"],
+                     "rows": mfma,
+                     "waves": blocks * 4, "mfmas_per_wave": iters * 4},
+            "compute_units": props.multi_processor_count}
 
 
 if __name__ == "__main__":

@@ -1,5 +1,7 @@
-"""Build the gfx950 C-ABI library libint8_linear_amd.so from csrc/*.hip, in-tree, and the
-host-only C++ binding _i8l_fast over it (csrc/i8l_torch.cpp).
+"""Build the gfx950 C-ABI library libint8_linear_amd.so from csrc/*.hip, in-tree, the
+host-only C++ binding _i8l_fast over it (csrc/i8l_torch.cpp), and the measurement probes
+bench.py times beside it (probes/i8l_floors.hip -> probes/libi8l_floors.so, not part of the
+W8A8 C ABI).
 
     python int8-linear_amd/build_lib.py
 
@@ -20,6 +22,8 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "int8_linear" / "libint8_linear_amd.so"
+PROBES_SRC = HERE / "probes" / "i8l_floors.hip"
+PROBES_LIB = HERE / "probes" / "libi8l_floors.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the epilogue and quantizer arithmetic is the sequence of IEEE ops
@@ -48,10 +52,12 @@ def build(verbose: bool = False) -> Path:
     returns the library's path."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    with ThreadPoolExecutor(max_workers=min(8, len(sources) + 1)) as ex:
+    with ThreadPoolExecutor(max_workers=min(8, len(sources) + 2)) as ex:
         binding = ex.submit(_compile_binding)
+        probes = ex.submit(_build_probes)
         objs = list(ex.map(_compile, sources))
         binding_obj = binding.result()
+        probes.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -67,6 +73,17 @@ def build(verbose: bool = False) -> Path:
 
 
 CXX = os.environ.get("CXX", "g++")
+
+
+def _build_probes() -> Path:
+    """The floor probes (empty launch, cold reads, MFMA loops) as their own library."""
+    tmp = PROBES_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-shared", str(PROBES_SRC), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PROBES_SRC.name}:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, PROBES_LIB)
+    return PROBES_LIB
 
 
 def _compile_binding() -> Path:

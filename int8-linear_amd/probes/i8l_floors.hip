@@ -1,0 +1,143 @@
+// Hardware floors measured beside the W8A8 kernels by bench.py (not part of the W8A8 C ABI):
+//
+//   fl_empty   an empty kernel: the cost of one launch in a HIP graph, at a given grid;
+//   fl_read    a pure read of `bytes` (16-byte loads, 1 to 8 a thread issued before any is
+//              used, no stores): the time to stream a weight matrix of that size, i.e. the
+//              floor under a decode GEMM that must read it once;
+//   fl_mfma    back-to-back v_mfma_i32_32x32x32_i8 (or v_mfma_i32_16x16x64_i8) on register
+//              operands, four independent accumulators a wave: the int8 MFMA rate the chip
+//              sustains under load, clock throttling included, on constant operands and on
+//              random ones (a GEMM's data toggles the multipliers, which costs power).
+//
+// Every kernel's grid covers exactly its work (the read kernel's grid is the buffer's blocks,
+// whose size divides it, so every load is in bounds), and results reach memory only through a
+// data-dependent store that never fires on the zeroed buffers bench.py passes, so no probe
+// writes more than its output of a few bytes.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int kReadThreads = 256;
+constexpr uint32_t kNeverSeen = 0x9e3779b9u;  // the XOR of zeroed memory is 0
+
+__global__ void fl_empty_kernel() {}
+
+// Each workgroup reads one block of U * 4 KiB: U 16-byte chunks a thread, the chunks of one
+// load instruction contiguous across the lanes (4 KiB a workgroup-wide load).
+template <int U>
+__global__ __launch_bounds__(kReadThreads) void fl_read_kernel(const uint4* __restrict__ src,
+                                                               uint32_t* __restrict__ out) {
+  const uint4* p = src + (int64_t)blockIdx.x * U * kReadThreads + threadIdx.x;
+  uint4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = p[u * kReadThreads];
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
+  uint32_t x = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  if (x == kNeverSeen) out[0] = x;
+}
+
+// RANDOM: the operands are two sets of random bytes read from `data` (2 KiB a set, 16 bytes a
+// lane), alternated so that every MFMA's inputs differ from the one before, as in a GEMM on
+// real data; otherwise constant operands (little toggles: the rate the MFMA pipes reach when
+// power is no limit).
+template <int KIND, bool RANDOM>
+__global__ __launch_bounds__(256) void fl_mfma_kernel(int iters, const v4i* __restrict__ data,
+                                                      int* __restrict__ out) {
+  const int t = threadIdx.x, lane = t & 63;
+  v4i a0 = {t, t + 1, t + 2, t + 3}, b0 = {t ^ 5, t ^ 6, t ^ 7, t ^ 9};
+  v4i a1 = b0, b1 = a0;
+  if constexpr (RANDOM) {
+    a0 = data[lane];
+    b0 = data[64 + lane];
+    a1 = data[128 + lane];
+    b1 = data[192 + lane];
+  }
+  if constexpr (KIND == 32) {
+    v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; ++i) {
+      c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, c3, 0, 0, 0);
+    }
+    const v16i s = c0 + c1 + c2 + c3;
+    int x = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x ^= s[j];
+    if (x == (int)kNeverSeen) out[0] = x;
+  } else {
+    v4i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; ++i) {
+      c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b1, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b0, c3, 0, 0, 0);
+    }
+    const v4i s = c0 + c1 + c2 + c3;
+    const int x = s[0] ^ s[1] ^ s[2] ^ s[3];
+    if (x == (int)kNeverSeen) out[0] = x;
+  }
+}
+
+int status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+
+}  // namespace
+
+extern "C" {
+
+// An empty kernel of `blocks` workgroups of `threads` (1..1024) on `stream`.
+int fl_empty(int blocks, int threads, void* stream) {
+  if (blocks < 1 || threads < 1 || threads > 1024) return -1;
+  hipLaunchKernelGGL(fl_empty_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream);
+  return status(hipGetLastError());
+}
+
+// Read `bytes` (a multiple of 32 KiB) at the 16-byte aligned `src` with `unroll` (1, 2, 4 or
+// 8) 16-byte loads a thread; `out` is one uint32.
+int fl_read(const void* src, int64_t bytes, uint32_t* out, int unroll, void* stream) {
+  if (bytes <= 0 || bytes % (32 << 10) || ((uintptr_t)src & 15)) return -1;
+  const int64_t blocks = bytes / (16LL * kReadThreads * unroll);
+  if (blocks > 0x7fffffff) return -1;
+  const dim3 grid((unsigned)blocks), block(kReadThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  const uint4* s = (const uint4*)src;
+  switch (unroll) {
+    case 1: hipLaunchKernelGGL(fl_read_kernel<1>, grid, block, 0, st, s, out); break;
+    case 2: hipLaunchKernelGGL(fl_read_kernel<2>, grid, block, 0, st, s, out); break;
+    case 4: hipLaunchKernelGGL(fl_read_kernel<4>, grid, block, 0, st, s, out); break;
+    case 8: hipLaunchKernelGGL(fl_read_kernel<8>, grid, block, 0, st, s, out); break;
+    default: return -1;
+  }
+  return status(hipGetLastError());
+}
+
+// `blocks` workgroups of 4 waves, each wave `iters` x 4 MFMAs of the given kind (32:
+// v_mfma_i32_32x32x32_i8, 65536 int ops each; 16: v_mfma_i32_16x16x64_i8, 32768 each).  With
+// `data` (4 KiB of random bytes, 16-byte aligned) the operands are those bytes; with NULL
+// they are constants.
+int fl_mfma(int kind, int blocks, int iters, const void* data, int* out, void* stream) {
+  if (blocks < 1 || iters < 1 || ((uintptr_t)data & 15)) return -1;
+  const dim3 grid(blocks), block(256);
+  const hipStream_t st = (hipStream_t)stream;
+  const v4i* d = (const v4i*)data;
+  if (kind == 32 && d)
+    hipLaunchKernelGGL((fl_mfma_kernel<32, true>), grid, block, 0, st, iters, d, out);
+  else if (kind == 32)
+    hipLaunchKernelGGL((fl_mfma_kernel<32, false>), grid, block, 0, st, iters, d, out);
+  else if (kind == 16 && d)
+    hipLaunchKernelGGL((fl_mfma_kernel<16, true>), grid, block, 0, st, iters, d, out);
+  else if (kind == 16)
+    hipLaunchKernelGGL((fl_mfma_kernel<16, false>), grid, block, 0, st, iters, d, out);
+  else
+    return -1;
+  return status(hipGetLastError());
+}
+
+}  // extern "C"
