@@ -230,7 +230,7 @@ def schedule_of(cfg, k: int) -> str:
         return "gemm_wlds1" if k == cfg.bk * cfg.warps else "gemm_wlds"
     if cfg.stages == 4 and cfg.bn <= 32:
         return "gemm_wlds1p"
-    return "gemm_dmap" if cfg.stages >= 11 else "gemm_dma"
+    return "gemm_dmap" if cfg.stages >= 10 else "gemm_dma"
 
 
 def copy_calibration(dev, mib: int = 256) -> dict:

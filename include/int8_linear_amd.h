@@ -50,9 +50,9 @@ enum {
  *                and bn <= 32 weights through LDS (decode); 4 with bn <= 32 the same in one
  *                K step a wave, each workgroup walking several column tiles with the
  *                activations held in registers (decode, K == bk * warps); 2 LDS staged
- *                through registers, 3..8 a ring of that many direct-to-LDS buffers, >= 11 the
- *                same ring of stages - 8 buffers with fragment reads overlapped with the
- *                MFMAs (prefill)
+ *                through registers, 3..8 a ring of that many direct-to-LDS buffers, >= 10 a
+ *                ring of stages - 8 buffers (2: a double buffer) with fragment reads
+ *                overlapped with the MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); with
  *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4)
  *   split_k    : reserved; must be 1

@@ -102,10 +102,13 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     return;
   }
   // Prefill: direct-to-LDS macro tiles with the fragment reads overlapped with the MFMAs
-  // (the fastest measured family on MI355X): 256x256 tiles once there are enough of them,
-  // 128x128 tiles (more workgroups) below.
+  // (the fastest measured family on MI355X): 256x256 tiles once there are enough of them
+  // (with 128-byte K steps, whole cache lines, in a double buffer when K allows), 128x128
+  // tiles (more workgroups) below.
   c->group_m = 8;
-  if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
+  if (N % 256 == 0 && K % 128 == 0 && M > 1024) {
+    *c = i8l_config{256, 256, 128, 8, 10, 4, 1};
+  } else if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
     *c = i8l_config{256, 256, 64, 8, 12, 4, 1};
   } else if (N % 128 == 0 && K % 128 == 0) {
     *c = i8l_config{128, 128, 128, 4, 12, 8, 1};
@@ -242,7 +245,7 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
     }
   } else if (c.stages == 2) {
     err = launch_staged(staged_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
-  } else if (c.stages >= 3 + kPipelined) {
+  } else if (c.stages >= 2 + kPipelined) {
     err = launch_dmap(dmap_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   } else {
     err = launch_dma(dma_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);

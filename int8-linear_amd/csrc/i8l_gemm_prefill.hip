@@ -318,6 +318,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// The same with lgkmcnt = 0 as well: this wave's LDS reads (and scalar loads) have returned.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
@@ -417,10 +424,13 @@ gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B
 // bytes is KK = BK/32 MFMA substeps; substep kk's MFMAs are issued one after another with the
 // reads of the next substep's fragments between them (one read after each MFMA), from two
 // register sets of one substep each.  Before the last substep of step t, each wave waits for
-// its DMA of step t+1 (vmcnt), the workgroup barrier makes step t+1 visible and frees the
-// buffer of step t-1 (whose last reads fed MFMAs before the barrier), and step t+S-1 is
-// requested into it; the last substep's MFMAs then overlap the reads of step t+1's first
-// substep.  The LDS traffic of each substep hides under the matrix work of the one before.
+// its own fragment reads of step t (lgkmcnt 0: the last substep's fragments are in registers,
+// so it is done with step t's buffer) and for its DMA of step t+1 (vmcnt); the workgroup
+// barrier then makes step t+1 visible and frees step t's buffer, and step t+S is requested
+// into it.  So all S buffers of the ring hold requested steps: step t+1 was requested S-1
+// steps of work before it is needed, and S = 2 is a double buffer.  The last substep's MFMAs
+// then overlap the reads of step t+1's first substep.  The LDS traffic of each substep hides
+// under the matrix work of the one before.
 template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
@@ -438,7 +448,7 @@ gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int NM = FA * FB;                // MFMAs per substep
   constexpr int NR = FA + FB;                // fragment reads per substep
-  static_assert(S >= 3, "the ring needs at least three buffers");
+  static_assert(S >= 2, "the ring needs at least two buffers");
 
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
@@ -515,11 +525,12 @@ gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     if (NR > P) __builtin_amdgcn_sched_group_barrier(0x100, NR - P, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Steps requested before the wait in step t: 0 .. t+S-2; step t+1 must be complete.
+  // Steps requested before the wait in step t: 0 .. t+S-1; step t+1 must be complete, and
+  // this wave's reads of step t's buffer done before the barrier lets it be refilled.
   auto turn = [&](int t) {
-    wait_vmcnt<J * (S - 3)>();
+    wait_vmcnt_lgkm0<J * (S - 2)>();
     lds_barrier();
-    dma(t + S - 1);
+    dma(t + S);
   };
   // One K step from fragment set 0 (holding substep 0); leaves step t+1's substep 0 in set 0
   // when `more`.  KK is even, so the substeps alternate 0,1,0,1,... and end in set 1.
@@ -539,8 +550,8 @@ gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   static_assert(KK % 2 == 0, "substeps alternate between the two fragment sets");
 
 #pragma unroll
-  for (int t = 0; t < S - 1; ++t) dma(t);
-  wait_vmcnt<J * (S - 2)>();
+  for (int t = 0; t < S; ++t) dma(t);
+  wait_vmcnt<J * (S - 1)>();
   lds_barrier();
   rd(f0a, f0b, 0, 0);
   for (int t = 0; t + 1 < KT; ++t) kstep(t, true);
@@ -587,10 +598,12 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {128, 64, 128, 2, 2, 4}, {128, 384, 64, 2, 4, 3},
                              {128, 384, 64, 2, 4, 4}, {128, 192, 64, 2, 2, 4},
                              {256, 192, 64, 2, 2, 4}, {64, 192, 64, 2, 2, 4},
-                             {64, 192, 128, 2, 2, 4}};
+                             {64, 192, 128, 2, 2, 4}, {256, 256, 128, 2, 4, 2},
+                             {256, 128, 128, 2, 4, 2}, {128, 256, 128, 2, 4, 2},
+                             {256, 192, 128, 4, 2, 2}};
 
 int dmap_index(const i8l_config& c) {
-  if (c.stages < 3 + kPipelined || c.split_k != 1 || c.group_m < 1) return -1;
+  if (c.stages < 2 + kPipelined || c.split_k != 1 || c.group_m < 1) return -1;
   for (int i = 0; i < (int)(sizeof(kDmap) / sizeof(kDmap[0])); ++i) {
     const auto& t = kDmap[i];
     if (t.bm == c.bm && t.bn == c.bn && t.bk == c.bk && t.wm * t.wn == c.warps &&
@@ -701,6 +714,10 @@ hipError_t launch_dmap(int idx, const i8l_config& c, const int8_t* a, int64_t ld
     case 18: return launch_dmap_t<256, 192, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 19: return launch_dmap_t<64, 192, 64, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
     case 20: return launch_dmap_t<64, 192, 128, 2, 2, 4>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 21: return launch_dmap_t<256, 256, 128, 2, 4, 2>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 22: return launch_dmap_t<256, 128, 128, 2, 4, 2>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 23: return launch_dmap_t<128, 256, 128, 2, 4, 2>(a, lda, b, ldb, e, K, c.group_m, st);
+    case 24: return launch_dmap_t<256, 192, 128, 4, 2, 2>(a, lda, b, ldb, e, K, c.group_m, st);
   }
   return hipErrorInvalidValue;
 }

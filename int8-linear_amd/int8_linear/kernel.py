@@ -48,8 +48,8 @@ class Config:
       stages == 2: double-buffered LDS staged through registers;
       3 <= stages <= 8, bm >= 128: a ring of `stages` LDS buffers filled by direct-to-LDS
         loads;
-      stages >= 11: the same ring of stages - 8 buffers with the LDS fragment reads of each
-        MFMA substep overlapped with the MFMAs of the one before.
+      stages >= 10: a ring of stages - 8 buffers (2 is a double buffer) with the LDS
+        fragment reads of each MFMA substep overlapped with the MFMAs of the one before.
     A configuration the library was not built with raises NotSupported.
     """
 

@@ -55,7 +55,9 @@ DMAP_TILES = [(256, 256, 64, 8, 3), (256, 256, 64, 8, 4), (256, 256, 64, 8, 5),
               (64, 128, 128, 4, 4), (64, 256, 128, 8, 3), (64, 128, 64, 4, 6),
               (64, 128, 128, 4, 6), (64, 64, 128, 4, 4), (128, 64, 128, 4, 4),
               (128, 384, 64, 8, 3), (128, 384, 64, 8, 4), (128, 192, 64, 4, 4),
-              (256, 192, 64, 4, 4), (64, 192, 64, 4, 4), (64, 192, 128, 4, 4)]
+              (256, 192, 64, 4, 4), (64, 192, 64, 4, 4), (64, 192, 128, 4, 4),
+              (256, 256, 128, 8, 2), (256, 128, 128, 8, 2), (128, 256, 128, 8, 2),
+              (256, 192, 128, 8, 2)]
 
 
 # (MT, NC, KS, W) of the built persistent single-step decode tiles (stages 4): K = 64*KS*W

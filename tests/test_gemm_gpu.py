@@ -75,7 +75,10 @@ TILINGS = [Config(16, 16, 64, 1, 1, 1), Config(32, 32, 256, 4, 1, 1), Config(64,
            Config(128, 128, 128, 4, 12, 8), Config(64, 128, 128, 4, 12, 8),
            Config(64, 256, 128, 8, 11, 4), Config(64, 128, 64, 4, 14, 1),
            Config(64, 128, 128, 4, 14, 8), Config(64, 64, 128, 4, 12, 8),
-           Config(128, 64, 128, 4, 12, 4)]
+           Config(128, 64, 128, 4, 12, 4),
+           # double-buffered (ring of two) with 128-byte K steps
+           Config(256, 256, 128, 8, 10, 4), Config(256, 128, 128, 8, 10, 8),
+           Config(128, 256, 128, 8, 10, 1)]
 
 
 @pytest.mark.parametrize("config", TILINGS, ids=lambda c: c.name.replace(" ", "_"))
@@ -202,7 +205,8 @@ def test_persistent_decode_tiles_exact(mt, nc, ks, w, m):
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
 # 12288), exact on N = 1536 with ragged M.
 WIDE_TILINGS = [Config(128, 384, 64, 8, 11, 4), Config(128, 384, 64, 8, 12, 8),
-                Config(128, 192, 64, 4, 12, 8), Config(256, 192, 64, 4, 12, 4)]
+                Config(128, 192, 64, 4, 12, 8), Config(256, 192, 64, 4, 12, 4),
+                Config(256, 192, 128, 8, 10, 4)]
 
 
 @pytest.mark.parametrize("config", WIDE_TILINGS, ids=lambda c: c.name.replace(" ", "_"))
@@ -454,7 +458,8 @@ def test_prefill_full_size_checksums_and_rows(shape):
 # tile of each prefill schedule (overlapped ring, ring, register-staged) and a 192-wide one.
 PREFILL_EPILOGUE_TILES = [Config(128, 128, 128, 4, 12, 8), Config(256, 256, 64, 8, 12, 4),
                           Config(256, 192, 64, 4, 12, 4), Config(256, 256, 64, 8, 3, 8),
-                          Config(128, 128, 64, 4, 2, 8)]
+                          Config(128, 128, 64, 4, 2, 8), Config(256, 256, 128, 8, 10, 4),
+                          Config(256, 192, 128, 8, 10, 4)]
 
 
 @pytest.mark.parametrize("config", PREFILL_EPILOGUE_TILES, ids=lambda c: c.name.replace(" ", "_"))
