@@ -55,11 +55,10 @@ enum {
  *                overlapped with the MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); with
  *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4)
- *   split_k    : reserved; must be 1
  * A config the library was not built for returns I8L_UNSUPPORTED.
  */
 typedef struct i8l_config {
-  int32_t bm, bn, bk, warps, stages, group_m, split_k;
+  int32_t bm, bn, bk, warps, stages, group_m;
 } i8l_config;
 
 /*

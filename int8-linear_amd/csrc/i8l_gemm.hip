@@ -22,14 +22,14 @@ gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_
 }
 
 void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
-  *c = i8l_config{0, 0, 0, 0, 0, 1, 1};
+  *c = i8l_config{0, 0, 0, 0, 0, 1};
   if (M <= 32 && K % 128 == 0) {
     const int mt = M <= 16 ? 1 : 2;
     // Many column tiles (N/16 >= 512) from 9 tokens: the persistent single-step tile with two
     // workgroups a CU, which loads the activations once a workgroup instead of once a tile.
     if (M > 8 && N % 16 == 0 && N / 16 >= 512) {
-      const i8l_config p = K == 4096 ? i8l_config{16 * mt, 8, 512, 8, 4, 2, 1}
-                                     : i8l_config{16 * mt, 16, 256, 8, 4, 2, 1};
+      const i8l_config p = K == 4096 ? i8l_config{16 * mt, 8, 512, 8, 4, 2}
+                                     : i8l_config{16 * mt, 16, 256, 8, 4, 2};
       if (wldsp_ok(p, K)) {
         *c = p;
         return;
@@ -44,14 +44,14 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     // the largest step that divides their slices
     for (int W : {8, 16, 4})
       for (int ks : kss) {
-        const i8l_config t{16 * mt, nc, 64 * ks, W, 3, 1, 1};
+        const i8l_config t{16 * mt, nc, 64 * ks, W, 3, 1};
         if (k64 == (int64_t)W * ks && wlds_ok(t, K)) {
           *c = t;
           return;
         }
       }
     for (int ks : kss) {
-      const i8l_config t{16 * mt, nc, 64 * ks, 16, 3, 1, 1};
+      const i8l_config t{16 * mt, nc, 64 * ks, 16, 3, 1};
       if (wlds_ok(t, K)) {
         *c = t;
         return;
@@ -68,18 +68,18 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
     for (const auto& t : tiles)
       if (N % t[1] == 0 && ((M + t[0] - 1) / t[0]) * (N / t[1]) >= 256) {
-        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8, 1};
+        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8};
         return;
       }
-    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8, 1};
+    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8};
     return;
   }
   // 17 to 128 tokens: weights through LDS in 32-token x 32-column tiles (several row
   // blocks above 32 tokens), 16 waves of one 128-byte step when K is 2048, else 4 waves
   // stepping through their K slices.
   if (M <= 128 && N % 32 == 0 && K % 128 == 0) {
-    const i8l_config one{32, 32, 128, 16, 3, 1, 1};
-    const i8l_config steps{32, 32, K % 1024 == 0 ? 256 : 128, 4, 3, 1, 1};
+    const i8l_config one{32, 32, 128, 16, 3, 1};
+    const i8l_config steps{32, 32, K % 1024 == 0 ? 256 : 128, 4, 3, 1};
     if (K == 2048 && N < 8192 && wlds_ok(one, K)) {
       *c = one;
       return;
@@ -107,18 +107,18 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   // tiles (more workgroups) below.
   c->group_m = 8;
   if (N % 256 == 0 && K % 128 == 0 && M > 1024) {
-    *c = i8l_config{256, 256, 128, 8, 10, 4, 1};
+    *c = i8l_config{256, 256, 128, 8, 10, 4};
   } else if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
-    *c = i8l_config{256, 256, 64, 8, 12, 4, 1};
+    *c = i8l_config{256, 256, 64, 8, 12, 4};
   } else if (N % 128 == 0 && K % 128 == 0) {
-    *c = i8l_config{128, 128, 128, 4, 12, 8, 1};
+    *c = i8l_config{128, 128, 128, 4, 12, 8};
   } else if (N % 128 == 0 && K % 64 == 0) {
-    *c = i8l_config{128, 128, 64, 4, 12, 8, 1};
+    *c = i8l_config{128, 128, 64, 4, 12, 8};
   } else {
     // narrow or odd shapes: the weight-streaming tile, one 128-token row block at a time
     int W = stream_max_threads(8, 1) / 64;
     while (W > 1 && K % (64 * W) != 0) W /= 2;
-    *c = i8l_config{128, 16, 64 * W, W, 1, 1, 1};
+    *c = i8l_config{128, 16, 64 * W, W, 1, 1};
   }
 }
 
@@ -148,8 +148,8 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
   }
   if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && dmap_index(c) < 0 &&
       !wlds_ok(c, K) && !wldsp_ok(c, K)) {
-    set_error("config %dx%dx%d w%d s%d g%d k%d is not built into this library", c.bm, c.bn,
-              c.bk, c.warps, c.stages, c.group_m, c.split_k);
+    set_error("config %dx%dx%d w%d s%d g%d is not built into this library", c.bm, c.bn,
+              c.bk, c.warps, c.stages, c.group_m);
     return I8L_UNSUPPORTED;
   }
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {

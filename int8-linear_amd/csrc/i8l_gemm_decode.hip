@@ -720,7 +720,7 @@ constexpr StreamTile kStream[] = {{1, 1, 16}, {2, 1, 16}, {4, 1, 16}, {8, 1, 16}
                                   {2, 2, 16}, {4, 2, 16}, {1, 1, 8},  {2, 1, 8},  {1, 1, 4}};
 
 bool stream_ok(const i8l_config& c) {
-  if (c.stages != 1 || c.split_k != 1 || c.bm % 16) return false;
+  if (c.stages != 1 || c.bm % 16) return false;
   if (c.warps < 1 || c.bk != 64 * c.warps) return false;
   for (auto t : kStream)
     if (t.mt * 16 == c.bm && t.nt * t.nc == c.bn) {
@@ -753,7 +753,7 @@ size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
 bool wlds1_built(int mt, int nc, int W, int ks);
 
 bool wlds_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 3 || c.split_k != 1 || c.bn > 32 || c.warps < 1 || c.warps > 16) return false;
+  if (c.stages != 3 || c.bn > 32 || c.warps < 1 || c.warps > 16) return false;
   bool built = false;
   for (auto t : kWlds)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
@@ -888,7 +888,7 @@ size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
 // group_m is the number of workgroups a compute unit runs at once (1, 2 or 4): all of them
 // must fit its LDS and its 2048 threads.
 bool wldsp_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 4 || c.split_k != 1 || c.bn > 32 ||
+  if (c.stages != 4 || c.bn > 32 ||
       (c.group_m != 1 && c.group_m != 2 && c.group_m != 4))
     return false;
   for (auto t : kWldsP)
@@ -987,7 +987,7 @@ size_t dq_lds_bytes(int nc, int ks, int W) {
 }
 
 bool dq_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 3 || c.split_k != 1 || c.bm != 16) return false;
+  if (c.stages != 3 || c.bm != 16) return false;
   for (auto t : kDq)
     if (t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
       return K == (int64_t)64 * t.ks * t.w && dq_lds_bytes(t.nc, t.ks, t.w) <= kMaxLds;
@@ -999,7 +999,7 @@ bool dq_ok(const i8l_config& c, int64_t K) {
 bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
   const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : 8;
   for (int ks : {2, 4}) {
-    const i8l_config t{16, nc, 64 * ks, 16, 3, 1, 1};
+    const i8l_config t{16, nc, 64 * ks, 16, 3, 1};
     if (K == (int64_t)64 * ks * 16 && dq_ok(t, K)) {
       *c = t;
       return true;

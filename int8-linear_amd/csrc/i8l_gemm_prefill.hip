@@ -603,7 +603,7 @@ constexpr DmaTile kDmap[] = {{256, 256, 64, 2, 4, 3}, {256, 256, 64, 2, 4, 4},
                              {256, 192, 128, 4, 2, 2}};
 
 int dmap_index(const i8l_config& c) {
-  if (c.stages < 2 + kPipelined || c.split_k != 1 || c.group_m < 1) return -1;
+  if (c.stages < 2 + kPipelined || c.group_m < 1) return -1;
   for (int i = 0; i < (int)(sizeof(kDmap) / sizeof(kDmap[0])); ++i) {
     const auto& t = kDmap[i];
     if (t.bm == c.bm && t.bn == c.bn && t.bk == c.bk && t.wm * t.wn == c.warps &&
@@ -614,7 +614,7 @@ int dmap_index(const i8l_config& c) {
 }
 
 int dma_index(const i8l_config& c) {
-  if (c.stages < 3 || c.split_k != 1 || c.group_m < 1) return -1;
+  if (c.stages < 3 || c.group_m < 1) return -1;
   for (int i = 0; i < (int)(sizeof(kDma) / sizeof(kDma[0])); ++i) {
     const auto& t = kDma[i];
     if (t.bm == c.bm && t.bn == c.bn && t.bk == c.bk && t.wm * t.wn == c.warps && t.s == c.stages)
@@ -624,7 +624,7 @@ int dma_index(const i8l_config& c) {
 }
 
 int staged_index(const i8l_config& c) {
-  if (c.stages != 2 || c.split_k != 1 || c.group_m < 1) return -1;
+  if (c.stages != 2 || c.group_m < 1) return -1;
   for (int i = 0; i < (int)(sizeof(kStaged) / sizeof(kStaged[0])); ++i) {
     const auto& t = kStaged[i];
     if (t.bm == c.bm && t.bn == c.bn && t.bk == c.bk && t.wm * t.wn == c.warps) return i;

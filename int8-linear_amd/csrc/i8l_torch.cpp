@@ -57,13 +57,13 @@ std::unordered_map<int, DeviceTable> g_tables;
 
 uint64_t kn_key(int64_t k, int64_t n) { return ((uint64_t)k << 32) ^ (uint64_t)n; }
 
-// rows: (k, n, m_bucket, bm, bn, bk, warps, stages, group_m, split_k)
+// rows: (k, n, m_bucket, bm, bn, bk, warps, stages, group_m)
 void set_table(int device, const std::vector<std::vector<int64_t>>& rows) {
   DeviceTable t;
   for (const auto& r : rows) {
-    TORCH_CHECK(r.size() == 10, "a tuned row has 10 fields");
+    TORCH_CHECK(r.size() == 9, "a tuned row has 9 fields");
     i8l_config c{(int32_t)r[3], (int32_t)r[4], (int32_t)r[5], (int32_t)r[6],
-                 (int32_t)r[7], (int32_t)r[8], (int32_t)r[9]};
+                 (int32_t)r[7], (int32_t)r[8]};
     t.shapes[kn_key(r[0], r[1])][r[2]] = c;
   }
   g_tables[device] = std::move(t);
@@ -86,12 +86,12 @@ bool choose(int device, int64_t m, int64_t n, int64_t k, i8l_config* c) {
   return i8l_default_config(m, n, k, c) == I8L_OK;
 }
 
-// The configuration the fast path launches (bm, bn, bk, warps, stages, group_m, split_k),
+// The configuration the fast path launches (bm, bn, bk, warps, stages, group_m),
 // or None before the device's table is handed over.
 py::object config_for(int device, int64_t m, int64_t n, int64_t k) {
   i8l_config c;
   if (!choose(device, m, n, k, &c)) return py::none();
-  return py::make_tuple(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, c.split_k);
+  return py::make_tuple(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m);
 }
 
 // Launches made through this module (every entry point), for tests that check it was used.

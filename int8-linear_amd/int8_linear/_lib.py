@@ -27,7 +27,7 @@ _I32 = ctypes.c_int32
 class CConfig(ctypes.Structure):
     """struct i8l_config (include/int8_linear_amd.h)."""
     _fields_ = [("bm", _I32), ("bn", _I32), ("bk", _I32), ("warps", _I32), ("stages", _I32),
-                ("group_m", _I32), ("split_k", _I32)]
+                ("group_m", _I32)]
 
 
 EXPORTS = ("i8l_w8a8_mm", "i8l_w8a8_mm_supported", "i8l_default_config",

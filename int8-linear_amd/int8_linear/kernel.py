@@ -59,12 +59,10 @@ class Config:
     warps: int = 4
     stages: int = 2
     group_m: int = 1
-    split_k: int = 1
 
     @property
     def name(self) -> str:
-        base = f"{self.bm}x{self.bn}x{self.bk} w{self.warps} s{self.stages} g{self.group_m}"
-        return base if self.split_k == 1 else f"{base} k{self.split_k}"
+        return f"{self.bm}x{self.bn}x{self.bk} w{self.warps} s{self.stages} g{self.group_m}"
 
 
 _cstructs: dict[Config, _lib.CConfig] = {}
@@ -74,7 +72,7 @@ def _cconfig(cfg: Config) -> _lib.CConfig:
     c = _cstructs.get(cfg)
     if c is None:
         c = _cstructs[cfg] = _lib.CConfig(cfg.bm, cfg.bn, cfg.bk, cfg.warps, cfg.stages,
-                                          cfg.group_m, cfg.split_k)
+                                          cfg.group_m)
     return c
 
 
@@ -84,7 +82,7 @@ def default_config(m: int, n: int, k: int) -> Config:
     up to 512, weight streaming otherwise up to 128 tokens, prefill macro tiles above."""
     c = _lib.CConfig()
     _lib.check(_lib.lib().i8l_default_config(m, n, k, c), NotSupported)
-    return Config(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, c.split_k)
+    return Config(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m)
 
 
 @lru_cache(maxsize=None)
@@ -126,15 +124,14 @@ def choose_config(m: int, n: int, k: int) -> Config:
 
 
 def _table_rows(device: int) -> list[list[int]]:
-    """This device's tuned table as rows (k, n, m, bm, bn, bk, warps, stages, group_m,
-    split_k), for the C++ binding's configuration lookup."""
+    """This device's tuned table as rows (k, n, m, bm, bn, bk, warps, stages, group_m), for the
+    C++ binding's configuration lookup."""
     rows = []
     for kn, buckets in _device_table(device).items():
         k, n = map(int, kn.split("x"))
         for m, row in buckets.items():
             c = Config(**row["config"])
-            rows.append([k, n, int(m), c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m,
-                         c.split_k])
+            rows.append([k, n, int(m), c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m])
     return rows
 
 

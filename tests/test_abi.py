@@ -110,7 +110,7 @@ def test_supported_decline_rule_matches_reference():
 
 
 def test_supported_reports_the_reason():
-    c = _lib.CConfig(16, 16, 64, 1, 1, 1, 1)
+    c = _lib.CConfig(16, 16, 64, 1, 1, 1)
     assert _lib.lib().i8l_w8a8_mm_supported(4, 64, 100, ctypes.byref(c)) == _lib.UNSUPPORTED
     assert "must divide" in _lib.last_error()
     with pytest.raises(NotSupported):
@@ -136,8 +136,14 @@ def test_invalid_sizes_are_rejected_before_any_launch():
 
 
 def test_config_name_format():
+    """The reference's Config fields and name format (int8_linear/kernel.py:49-60)."""
+    import dataclasses
     assert Config(16, 64, 64, 4, 1, 1).name == "16x64x64 w4 s1 g1"
-    assert Config(256, 256, 64, 4, 2, 8, 2).name == "256x256x64 w4 s2 g8 k2"
+    assert Config(256, 256, 64, 4, 2, 8).name == "256x256x64 w4 s2 g8"
+    assert [f.name for f in dataclasses.fields(Config)] == ["bm", "bn", "bk", "warps", "stages",
+                                                             "group_m"]
+    assert [f for f, _ in _lib.CConfig._fields_] == ["bm", "bn", "bk", "warps", "stages",
+                                                     "group_m"]
 
 
 def test_tuned_config_takes_the_largest_bucket_at_or_below_m(monkeypatch):
@@ -180,7 +186,7 @@ def test_cpp_binding_loads_and_chooses_the_tuned_config():
     assert f is not None, "the binding is built with the library"
     for name in ("mm", "add_rmsnorm_quant", "silu_mul_quant", "quant_per_token", "set_table"):
         assert hasattr(f, name)
-    rows = [[2048, 4096, 1, 16, 16, 512, 8, 1, 1, 1], [2048, 4096, 17, 32, 16, 512, 8, 1, 1, 1]]
+    rows = [[2048, 4096, 1, 16, 16, 512, 8, 1, 1], [2048, 4096, 17, 32, 16, 512, 8, 1, 1]]
     f.set_table(7, rows)
     assert f.has_table(7) and not f.has_table(6)
     assert f.config_for(6, 1, 4096, 2048) is None
@@ -190,8 +196,7 @@ def test_cpp_binding_loads_and_chooses_the_tuned_config():
     assert f.config_for(7, 500, 4096, 2048)[:2] == (32, 16)
     for m, n, k in ((5, 2048, 2048), (4096, 4096, 4096), (96, 12288, 2048)):
         d = kn.default_config(m, n, k)
-        assert f.config_for(7, m, n, k) == (d.bm, d.bn, d.bk, d.warps, d.stages, d.group_m,
-                                            d.split_k)
+        assert f.config_for(7, m, n, k) == (d.bm, d.bn, d.bk, d.warps, d.stages, d.group_m)
 
 
 def test_cpp_binding_declines_what_the_python_path_must_handle():
@@ -213,9 +218,9 @@ def test_dynamic_quant_entry_validates_on_the_host():
     assert L.i8l_w8a8_mm_dynq_supported(1, 4096, 4096, None) == _lib.OK
     assert L.i8l_w8a8_mm_dynq_supported(4, 2048, 6144, None) == _lib.UNSUPPORTED
     assert "one step" in _lib.last_error()
-    c = _lib.CConfig(16, 32, 128, 16, 3, 1, 1)
+    c = _lib.CConfig(16, 32, 128, 16, 3, 1)
     assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, ctypes.byref(c)) == _lib.OK
-    c = _lib.CConfig(16, 32, 128, 8, 3, 1, 1)                  # two steps a wave: not built
+    c = _lib.CConfig(16, 32, 128, 8, 3, 1)                     # two steps a wave: not built
     assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, ctypes.byref(c)) == _lib.UNSUPPORTED
     # argument errors come back before anything launches (no pointer is touched)
     args = [None, 2048, _lib.BF16, 1, None, 1, 2048, None, 7, None, 0, None, 2048, _lib.BF16,

@@ -46,7 +46,7 @@ def test_mm_binding_equals_ctypes_path(m, k, n, bias_dtype, ctypes_only):
     assert fast().launches() == before + 1
     cfg = choose_config(m, n, k)
     assert fast().config_for(a.get_device(), m, n, k) == (cfg.bm, cfg.bn, cfg.bk, cfg.warps,
-                                                          cfg.stages, cfg.group_m, cfg.split_k)
+                                                          cfg.stages, cfg.group_m)
     ctypes_only()
     ref = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, bias)
     torch.cuda.synchronize()
