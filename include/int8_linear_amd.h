@@ -168,6 +168,37 @@ int i8l_w8a8_mm_dynq(const void* x, int64_t ldx, int32_t act_dtype, int32_t prec
 /* Whether i8l_w8a8_mm_dynq takes (M,N,K,cfg) (cfg NULL: the library's choice); host-only. */
 int i8l_w8a8_mm_dynq_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
 
+/*
+ * The SiLU-and-mul quantizer and the W8A8 matmul in one launch, for few tokens:
+ *   out = i8l_w8a8_mm(q, b, scale_a = s, scale_b, bias)  with  (q, s) = silu_mul_quant(gate_up)
+ * bit for bit (i8l_silu_mul_quant with the same round_silu and precise_div).  gate_up is
+ * bf16/f16 [M, 2K] with row stride ldgu (a multiple of 8 elements, >= 2K) and a 16-byte aligned
+ * base: the gate values in columns [0, K), the up values in [K, 2K); K is the matmul's K (the
+ * MLP's intermediate size) and a multiple of 8.  Every column tile computes the SiLU-and-mul
+ * and the row scales of its token rows itself, so the work grows with M times the number of
+ * column tiles: M is at most 8 (larger M returns I8L_UNSUPPORTED; use the two calls).
+ * scale_a_out, if not NULL, receives the M per-token scales.  b must be K-contiguous
+ * (stride_bk == 1) and 16-byte aligned, out 16-byte aligned with 16-byte row pitch.  cfg is a
+ * single-step weights-through-LDS tile of the SiLU form (bm 16, bn 8, bk 512, 12 waves,
+ * stages 3, K == 12 * 512) or NULL for the library's choice.
+ *
+ * Replaces the pair the reference's stand-in issues per down_proj, silu_mul_quant then
+ * _w8a8_mm (bench/fuse_quant.py:238-240 of AshrithaG/int8-linear; fused_quant.py:113-124 and
+ * kernel.py:202-257).
+ */
+int i8l_silu_mul_quant_mm(const void* gate_up, int64_t ldgu, int32_t act_dtype,
+                          int32_t round_silu, int32_t precise_div,
+                          const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                          const float* scale_b, int64_t scale_b_len,
+                          const void* bias, int32_t bias_dtype,
+                          void* out, int64_t stride_cm, int32_t out_dtype, float* scale_a_out,
+                          int64_t M, int64_t N, int64_t K,
+                          const i8l_config* cfg, void* stream);
+
+/* Whether i8l_silu_mul_quant_mm takes (M,N,K,cfg) (cfg NULL: the library's choice);
+ * host-only. */
+int i8l_silu_mul_quant_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
+
 /* Thread-local description of the last failure ("" if none). */
 const char* i8l_last_error(void);
 

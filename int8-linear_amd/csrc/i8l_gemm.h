@@ -244,9 +244,16 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
                         int64_t ldb, const Epi& e, hipStream_t st);
 bool dq_ok(const i8l_config& c, int64_t K);
 bool default_dq_config(int64_t N, int64_t K, i8l_config* c);
+bool dq_silu_ok(const i8l_config& c, int64_t K);
+bool default_dq_silu_config(int64_t N, int64_t K, i8l_config* c);
+int dq_silu_max_rows();
 hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
                      const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
                      hipStream_t st);
+hipError_t launch_dq_silu(const i8l_config& c, int act_dtype, int round_silu,
+                          const uint16_t* gate_up, int64_t ldgu, int64_t up, const int8_t* b,
+                          int64_t ldb, const Epi& e, float* sa_out, int precise,
+                          hipStream_t st);
 // Prefill (i8l_gemm_prefill.hip): the index of a config among the built tiles, or -1.
 int staged_index(const i8l_config& c);
 int dma_index(const i8l_config& c);

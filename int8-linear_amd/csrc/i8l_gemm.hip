@@ -345,3 +345,101 @@ extern "C" int i8l_w8a8_mm_dynq(const void* x, int64_t ldx, int32_t act_dtype,
                                    scale_a_out, precise_div ? 1 : 0, (hipStream_t)stream);
   return hip_status(err, "i8l_w8a8_mm_dynq launch");
 }
+
+extern "C" int i8l_silu_mul_quant_mm_supported(int64_t M, int64_t N, int64_t K,
+                                               const i8l_config* cfg) {
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_dq_silu_config(N, K, &c)) {
+    set_error("no built SiLU-and-mul quant tile takes K=%lld, N=%lld", (long long)K,
+              (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  if (M < 0 || M > dq_silu_max_rows() || N > INT32_MAX || K > INT32_MAX) {
+    set_error("the SiLU-and-mul quant matmul takes up to %d tokens, got %lld",
+              dq_silu_max_rows(), (long long)M);
+    return I8L_UNSUPPORTED;
+  }
+  if (c.bn <= 0 || N % c.bn || !dq_silu_ok(c, K)) {
+    set_error("config %dx%dx%d w%d s%d is not a built SiLU-and-mul quant tile for N=%lld K=%lld",
+              c.bm, c.bn, c.bk, c.warps, c.stages, (long long)N, (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  return I8L_OK;
+}
+
+extern "C" int i8l_silu_mul_quant_mm(const void* gate_up, int64_t ldgu, int32_t act_dtype,
+                                     int32_t round_silu, int32_t precise_div, const int8_t* b,
+                                     int64_t stride_bk, int64_t stride_bn, const float* scale_b,
+                                     int64_t scale_b_len, const void* bias, int32_t bias_dtype,
+                                     void* out, int64_t stride_cm, int32_t out_dtype,
+                                     float* scale_a_out, int64_t M, int64_t N, int64_t K,
+                                     const i8l_config* cfg, void* stream) {
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("negative size M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    return I8L_INVALID_ARG;
+  }
+  if (act_dtype != I8L_BF16 && act_dtype != I8L_F16) {
+    set_error("activations must be bf16 or fp16 (code %d)", act_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (out_dtype != I8L_BF16 && out_dtype != I8L_F16 && out_dtype != I8L_F32) {
+    set_error("unsupported output dtype code %d", out_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (scale_b_len != 1 && scale_b_len != N) {
+    set_error("scale_b has %lld values for N=%lld", (long long)scale_b_len, (long long)N);
+    return I8L_INVALID_ARG;
+  }
+  if (bias_dtype != I8L_DTYPE_NONE && bias_dtype != I8L_BF16 && bias_dtype != I8L_F16 &&
+      bias_dtype != I8L_F32) {
+    set_error("unsupported bias dtype code %d", bias_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if ((bias_dtype == I8L_DTYPE_NONE) != (bias == nullptr)) {
+    set_error("bias pointer and bias dtype disagree");
+    return I8L_INVALID_ARG;
+  }
+  if (ldgu < 2 * K) {
+    set_error("row stride %lld of gate_up is below 2K=%lld", (long long)ldgu, (long long)(2 * K));
+    return I8L_INVALID_ARG;
+  }
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_dq_silu_config(N, K, &c)) {
+    set_error("no built SiLU-and-mul quant tile takes K=%lld, N=%lld", (long long)K,
+              (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  const int st = i8l_silu_mul_quant_mm_supported(M, N, K, &c);
+  if (st != I8L_OK) return st;
+  if (M == 0 || N == 0) return I8L_OK;
+  const int osz = elt_size(out_dtype);
+  const bool layout = stride_bk == 1 && aligned16(b) && stride_bn % 16 == 0 &&
+                      stride_bn <= INT32_MAX / 32 && aligned16(gate_up) && ldgu % 8 == 0 &&
+                      K % 8 == 0 && aligned16(out) && (stride_cm * osz) % 16 == 0 &&
+                      stride_cm >= N && N % 4 == 0 && (scale_b_len == 1 || aligned16(scale_b)) &&
+                      (bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
+  if (!layout) {
+    set_error("the SiLU-and-mul quant path needs K-contiguous 16-byte aligned operands");
+    return I8L_UNSUPPORTED;
+  }
+  Epi e;
+  e.sa = nullptr;
+  e.sb = scale_b;
+  e.bias = bias;
+  e.out = out;
+  e.ldc = stride_cm;
+  e.sa_per_row = 1;
+  e.sb_per_col = scale_b_len == N && N > 1;
+  e.bias_dtype = bias_dtype;
+  e.out_dtype = out_dtype;
+  e.M = (int)M;
+  e.N = (int)N;
+  const hipError_t err = launch_dq_silu(c, act_dtype, round_silu ? 1 : 0,
+                                        (const uint16_t*)gate_up, ldgu, K, b, stride_bn, e,
+                                        scale_a_out, precise_div ? 1 : 0, (hipStream_t)stream);
+  return hip_status(err, "i8l_silu_mul_quant_mm launch");
+}

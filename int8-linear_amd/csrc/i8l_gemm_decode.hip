@@ -555,10 +555,20 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // rows: a wave reads its slice as 16-byte chunks of 8 values, CH = S/8 chunks a row and
 // 64/CH rows a pass over the lanes, quantizes them, and writes the codes to an LDS tile of
 // 16 rows x S bytes, from which the MFMA fragments are read (rows past M read as zero).
-template <int NC, int KS, int W, int P, int EK, int DT>
+//
+// ACT selects what is quantized.  kActPlain: X itself.  kActSilu / kActSiluRound: the
+// SiLU-and-mul of a gate_up row, X holding the gate values and X + up the up values of the
+// same row: y = cast(silu(g) * u), with silu(g) = g / (1 + exp(-g)) from the canonical exp
+// and a correctly rounded quotient, rounded to the activation dtype first for kActSiluRound;
+// these are the silu_mul_quant kernel's values, so the output equals silu_mul_quant followed
+// by w8a8_mm bit for bit (reference fused_quant.py:76-88 then kernel.py:63-124).
+enum { kActPlain = 0, kActSilu = 1, kActSiluRound = 2 };
+
+template <int NC, int KS, int W, int P, int EK, int DT, int ACT>
 __global__ void __launch_bounds__(64 * W)
-gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ B,
-              int64_t ldb, Epi e, float* __restrict__ sa_out, int precise) {
+gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
+              const int8_t* __restrict__ B, int64_t ldb, Epi e, float* __restrict__ sa_out,
+              int precise) {
   constexpr int S = 64 * KS;
   constexpr int CPR = S / 16;
   constexpr int CPR_LOW = CPR & -CPR;
@@ -596,12 +606,18 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restr
   // then runs while the weights' DMA is still in flight.
   // pass p: lane l holds chunk l % CH of row p*RPP + l/CH (rows past M are not read)
   const int crow = lane / CH, cchunk = lane % CH;
-  uint4 xr[P];
+  constexpr bool SILU = ACT != kActPlain;
+  uint4 xr[P], ur[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     xr[p] = uint4{0, 0, 0, 0};
+    ur[p] = uint4{0, 0, 0, 0};
     const int r = p * RPP + crow;
-    if (r < mb) xr[p] = *(const uint4*)(X + (m0 + r) * ldx + kw + 8 * cchunk);
+    if (r < mb) {
+      const uint16_t* src = X + (m0 + r) * ldx + kw + 8 * cchunk;
+      xr[p] = *(const uint4*)src;
+      if constexpr (SILU) ur[p] = *(const uint4*)(src + up);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   const int8_t* Bw = B + n0 * ldb + kw;
@@ -621,12 +637,63 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restr
     const uint32_t w32 = k < 4 ? (k < 2 ? v.x : v.y) : (k < 6 ? v.z : v.w);
     return act_to_f32<DT>((k & 1) ? (w32 >> 16) : (w32 & 0xffffu));
   };
+  // the values to quantize, computed once (rows past M hold zeros, silu(0) * 0 = 0)
+  float y[P][8];
+  // silu(g) = g / d with d = 1 + exp(-g): the quotient as rcp(d) with one Newton-Markstein
+  // correction and g's sign, which equals IEEE division for every bf16 and fp16 g in
+  // (-87, +inf) (the silu_mul_quant kernel's fast form); a wave holding any other g takes
+  // IEEE division for all of its values.
+  auto silu = [&](float g, bool ieee) -> float {
+    const float d = 1.0f + canon_expf_core(__builtin_amdgcn_fmed3f(-g, -87.5f, 89.5f));
+    float a;
+    if (ieee) {
+      a = g / d;
+    } else {
+      const float r0 = __builtin_amdgcn_rcpf(d);
+      const float q0 = g * r0;
+      const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r0, q0);
+      a = __uint_as_float((__float_as_uint(q1) & 0x7fffffffu) | (__float_as_uint(g) & 0x80000000u));
+    }
+    return a;
+  };
+  auto fill = [&](bool ieee) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        float a0 = elem(xr[p], k), a1 = elem(xr[p], k + 1);
+        if constexpr (SILU) {
+          a0 = silu(a0, ieee);
+          a1 = silu(a1, ieee);
+          if constexpr (ACT == kActSiluRound) round_through2<DT>(a0, a1);
+          a0 = a0 * elem(ur[p], k);
+          a1 = a1 * elem(ur[p], k + 1);
+          round_through2<DT>(a0, a1);
+        }
+        y[p][k] = a0;
+        y[p][k + 1] = a1;
+      }
+    }
+  };
+  if constexpr (SILU) {
+    float gmin = __builtin_inff(), gmax = -__builtin_inff();
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        gmin = fminf(gmin, elem(xr[p], k));
+        gmax = fmaxf(gmax, elem(xr[p], k));
+      }
+    fill(!__all(gmin > -87.0f && gmax < __builtin_inff()));
+  } else {
+    fill(false);
+  }
   // absmax of each valid row's slice: a lane's chunk, then the CH lanes of the row
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     float am = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(elem(xr[p], k)));
+    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(y[p][k]));
     am = group_max<CH>(am);
     if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
   }
@@ -655,7 +722,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, const int8_t* __restr
         uint32_t packed = 0;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          float v = __builtin_rintf(elem(xr[p], 4 * q + b) * inv);
+          float v = __builtin_rintf(y[p][4 * q + b] * inv);
           v = fminf(fmaxf(v, -128.0f), 127.0f);
           packed |= ((uint32_t)(int)v & 0xffu) << (8 * b);
         }
@@ -978,6 +1045,12 @@ struct DqTile {
   int nc, ks, w;
 };
 constexpr DqTile kDq[] = {{8, 2, 16}, {16, 2, 16}, {32, 2, 16}, {8, 4, 16}, {16, 4, 16}};
+// The SiLU-and-mul form's tiles (gate_up rows of 2K values feeding K = 64 * KS * W): 12 waves
+// of 512-byte slices take Qwen3-1.7B's K = 6144 (a slice of 384 bytes would not split the
+// 8-value chunks of a row over the lanes).  One 16-token row block with at most 8 valid
+// rows: the row values stay in registers.
+constexpr DqTile kDqSilu[] = {{8, 8, 12}};
+constexpr int kDqSiluMaxRows = 8;
 
 size_t dq_lds_bytes(int nc, int ks, int W) {
   const int nf = nc > 16 ? nc / 16 : 1;
@@ -1008,54 +1081,82 @@ bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
   return false;
 }
 
-template <int NC, int KS, int W, int P, int EK, int DT>
-hipError_t launch_dq_k(const uint16_t* x, int64_t ldx, const int8_t* b, int64_t ldb,
-                       const Epi& e, float* sa_out, int precise, hipStream_t st) {
-  auto kern = gemm_wlds1_dq<NC, KS, W, P, EK, DT>;
+bool dq_silu_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 3 || c.bm != 16) return false;
+  for (auto t : kDqSilu)
+    if (t.nc == c.bn && 64 * t.ks == c.bk && t.w == c.warps)
+      return K == (int64_t)64 * t.ks * t.w && dq_lds_bytes(t.nc, t.ks, t.w) <= kMaxLds;
+  return false;
+}
+
+bool default_dq_silu_config(int64_t N, int64_t K, i8l_config* c) {
+  for (auto t : kDqSilu) {
+    const i8l_config cand{16, t.nc, 64 * t.ks, t.w, 3, 1};
+    if (N % t.nc == 0 && dq_silu_ok(cand, K)) {
+      *c = cand;
+      return true;
+    }
+  }
+  return false;
+}
+
+int dq_silu_max_rows() { return kDqSiluMaxRows; }
+
+template <int NC, int KS, int W, int P, int EK, int DT, int ACT>
+hipError_t launch_dq_k(const uint16_t* x, int64_t ldx, int64_t up, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+  auto kern = gemm_wlds1_dq<NC, KS, W, P, EK, DT, ACT>;
   const size_t shm = dq_lds_bytes(NC, KS, W);
   static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
   lds_opt_in((const void*)kern, shm, lds_done);
   const dim3 grid(e.N / NC, (e.M + 15) / 16);
-  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, x, ldx, b, ldb, e, sa_out, precise);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, x, ldx, up, b, ldb, e, sa_out, precise);
   return hipGetLastError();
 }
 
-template <int NC, int KS, int W, int P>
-hipError_t launch_dq_p(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
-                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+template <int NC, int KS, int W, int P, int ACT>
+hipError_t launch_dq_p(int act_dtype, const uint16_t* x, int64_t ldx, int64_t up,
+                       const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
+                       hipStream_t st) {
   if (act_dtype == I8L_F16)
-    return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_F16>(x, ldx, b, ldb, e, sa_out, precise, st);
+    return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_F16, ACT>(x, ldx, up, b, ldb, e, sa_out,
+                                                           precise, st);
   switch (epi_kind(e)) {
     case EK_BF16:
-      return launch_dq_k<NC, KS, W, P, EK_BF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
-                                                          st);
+      return launch_dq_k<NC, KS, W, P, EK_BF16, I8L_BF16, ACT>(x, ldx, up, b, ldb, e, sa_out,
+                                                               precise, st);
     case EK_BF16_BBF16:
-      return launch_dq_k<NC, KS, W, P, EK_BF16_BBF16, I8L_BF16>(x, ldx, b, ldb, e, sa_out,
-                                                                precise, st);
+      return launch_dq_k<NC, KS, W, P, EK_BF16_BBF16, I8L_BF16, ACT>(x, ldx, up, b, ldb, e,
+                                                                     sa_out, precise, st);
     default:
-      return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_BF16>(x, ldx, b, ldb, e, sa_out, precise,
-                                                         st);
+      return launch_dq_k<NC, KS, W, P, EK_ANY, I8L_BF16, ACT>(x, ldx, up, b, ldb, e, sa_out,
+                                                              precise, st);
   }
 }
 
 // Passes of the quantizer prologue: ceil(rows / RPP) for the block's valid rows, taken as
-// the next power of two (P in {1, 2, 4, ...}, at most 16 rows).
-template <int NC, int KS, int W>
-hipError_t launch_dq_t(int act_dtype, const uint16_t* x, int64_t ldx, const int8_t* b,
-                       int64_t ldb, const Epi& e, float* sa_out, int precise, hipStream_t st) {
+// the next power of two (P in {1, 2, 4, ...}, at most 16 rows, or MAXR for the SiLU form).
+template <int NC, int KS, int W, int ACT, int MAXR>
+hipError_t launch_dq_t(int act_dtype, const uint16_t* x, int64_t ldx, int64_t up,
+                       const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
+                       hipStream_t st) {
   constexpr int RPP = 64 / (8 * KS);
   const int rows = e.M < 16 ? e.M : 16;
   const int need = (rows + RPP - 1) / RPP;
   if (need <= 1)
-    return launch_dq_p<NC, KS, W, 1>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+    return launch_dq_p<NC, KS, W, 1, ACT>(act_dtype, x, ldx, up, b, ldb, e, sa_out, precise,
+                                          st);
   if (need <= 2)
-    return launch_dq_p<NC, KS, W, 2>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
-  if constexpr (16 / RPP >= 4)
+    return launch_dq_p<NC, KS, W, 2, ACT>(act_dtype, x, ldx, up, b, ldb, e, sa_out, precise,
+                                          st);
+  if constexpr (MAXR / RPP >= 4)
     if (need <= 4)
-      return launch_dq_p<NC, KS, W, 4>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
-  if constexpr (16 / RPP >= 8)
+      return launch_dq_p<NC, KS, W, 4, ACT>(act_dtype, x, ldx, up, b, ldb, e, sa_out, precise,
+                                            st);
+  if constexpr (MAXR / RPP >= 8)
     if (need <= 8)
-      return launch_dq_p<NC, KS, W, 8>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+      return launch_dq_p<NC, KS, W, 8, ACT>(act_dtype, x, ldx, up, b, ldb, e, sa_out, precise,
+                                            st);
   return hipErrorInvalidValue;
 }
 
@@ -1065,9 +1166,29 @@ hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int6
   const int nc = c.bn, ks = c.bk / 64, W = c.warps;
 #define I8L_DQ(NC_, KS_, W_)                                                                \
   if (nc == NC_ && ks == KS_ && W == W_)                                                    \
-    return launch_dq_t<NC_, KS_, W_>(act_dtype, x, ldx, b, ldb, e, sa_out, precise, st);
+    return launch_dq_t<NC_, KS_, W_, kActPlain, 16>(act_dtype, x, ldx, 0, b, ldb, e, sa_out, \
+                                                    precise, st);
   I8L_DQ(8, 2, 16) I8L_DQ(16, 2, 16) I8L_DQ(32, 2, 16) I8L_DQ(8, 4, 16) I8L_DQ(16, 4, 16)
 #undef I8L_DQ
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dq_silu(const i8l_config& c, int act_dtype, int round_silu,
+                          const uint16_t* gate_up, int64_t ldgu, int64_t up, const int8_t* b,
+                          int64_t ldb, const Epi& e, float* sa_out, int precise,
+                          hipStream_t st) {
+  if (e.M > kDqSiluMaxRows) return hipErrorInvalidValue;
+  const int nc = c.bn, ks = c.bk / 64, W = c.warps;
+#define I8L_DQS(NC_, KS_, W_)                                                               \
+  if (nc == NC_ && ks == KS_ && W == W_)                                                    \
+    return round_silu                                                                       \
+        ? launch_dq_t<NC_, KS_, W_, kActSiluRound, kDqSiluMaxRows>(                         \
+              act_dtype, gate_up, ldgu, up, b, ldb, e, sa_out, precise, st)                 \
+        : launch_dq_t<NC_, KS_, W_, kActSilu, kDqSiluMaxRows>(act_dtype, gate_up, ldgu, up, \
+                                                              b, ldb, e, sa_out, precise,   \
+                                                              st);
+  I8L_DQS(8, 8, 12)
+#undef I8L_DQS
   return hipErrorInvalidValue;
 }
 

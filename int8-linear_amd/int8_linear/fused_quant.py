@@ -8,6 +8,7 @@ that quantizer into the op that produces the input, one workgroup per token row:
     silu_mul_quant(gate_up)                -> (x_q, scale)
     quant_per_token(x)                     -> (x_q, scale)
     quant_mm(x, b_q, scale_b)              -> w8a8_mm(*quant_per_token(x), b_q, ...)
+    silu_mul_quant_mm(gate_up, b_q, ...)   -> w8a8_mm(*silu_mul_quant(gate_up), b_q, ...)
 
 Same Python surface and arithmetic as the reference's int8_linear/fused_quant.py
 (AshrithaG/int8-linear, 41-124): residual add and norm in fp32, the normalized value rounded
@@ -136,31 +137,13 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
 QUANT_MM_MAX_M = 8
 
 
-def quant_mm(x: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
-             out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None,
-             precise_div: bool = True, *, config=None, return_scale: bool = False):
-    """quant_per_token(x) followed by w8a8_mm, as one kernel, for up to QUANT_MM_MAX_M tokens.
-
-    Bit for bit w8a8_mm(*quant_per_token(x, precise_div), b_q, ..., scale_b, out_dtype,
-    bias): the same quantizer arithmetic runs inside the GEMM (reference fused_quant.py:41-53
-    and kernel.py:202-257 in one launch).  x is bf16/fp16 [M, K], contiguous or a column
-    slice with unit column stride; b_q the K-contiguous [K, N] view of an [N, K] weight.
-    Raises NotSupported for more tokens, for a K that no single-step tile takes, or for
-    layouts the fused kernel does not read (the caller then makes the two calls).
-    """
-    from int8_linear.kernel import Config, _cconfig
-    if x.dim() != 2 or b_q.dim() != 2 or x.shape[1] != b_q.shape[0]:
-        raise ValueError(f"cannot multiply {tuple(x.shape)} by {tuple(b_q.shape)}")
-    act = _act_code(x, "x")
+def _mm_operands(x, b_q, scale_b, bias, out_dtype, what):
+    """Checks shared by the folded-quantizer matmuls: returns (N, scale_b flat, bias or None,
+    bias dtype code, output dtype code), or raises the reference's exception."""
     if b_q.dtype != torch.int8 or not b_q.is_cuda:
-        raise NotSupported("b_q must be an int8 HIP tensor")
+        raise NotSupported(f"{what}: b_q must be an int8 HIP tensor")
     same_device(x.device, b_q=b_q, scale_b=scale_b, bias=bias)
-    M, K = x.shape
     N = b_q.shape[1]
-    if M > QUANT_MM_MAX_M:
-        raise NotSupported(f"quant_mm takes up to {QUANT_MM_MAX_M} tokens, got {M}")
-    if x.stride(1) != 1 and K > 1:
-        raise NotSupported("x needs a unit column stride")
     sb = scale_b.reshape(-1).contiguous()
     if sb.dtype != torch.float32:
         raise NotSupported(f"float32 scale_b only, got {sb.dtype}")
@@ -178,6 +161,31 @@ def quant_mm(x: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
     out_code = _lib.DTYPE_CODE.get(out_dtype)
     if out_code not in (_lib.BF16, _lib.F16, _lib.F32):
         raise NotSupported(f"output dtype {out_dtype} is not supported")
+    return N, sb, bias, bias_code, out_code
+
+
+def quant_mm(x: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
+             out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None,
+             precise_div: bool = True, *, config=None, return_scale: bool = False):
+    """quant_per_token(x) followed by w8a8_mm, as one kernel, for up to QUANT_MM_MAX_M tokens.
+
+    Bit for bit w8a8_mm(*quant_per_token(x, precise_div), b_q, ..., scale_b, out_dtype,
+    bias): the same quantizer arithmetic runs inside the GEMM (reference fused_quant.py:41-53
+    and kernel.py:202-257 in one launch).  x is bf16/fp16 [M, K], contiguous or a column
+    slice with unit column stride; b_q the K-contiguous [K, N] view of an [N, K] weight.
+    Raises NotSupported for more tokens, for a K that no single-step tile takes, or for
+    layouts the fused kernel does not read (the caller then makes the two calls).
+    """
+    from int8_linear.kernel import Config, _cconfig
+    if x.dim() != 2 or b_q.dim() != 2 or x.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(x.shape)} by {tuple(b_q.shape)}")
+    act = _act_code(x, "x")
+    M, K = x.shape
+    if M > QUANT_MM_MAX_M:
+        raise NotSupported(f"quant_mm takes up to {QUANT_MM_MAX_M} tokens, got {M}")
+    if x.stride(1) != 1 and K > 1:
+        raise NotSupported("x needs a unit column stride")
+    N, sb, bias, bias_code, out_code = _mm_operands(x, b_q, scale_b, bias, out_dtype, "quant_mm")
     out = torch.empty((M, N), dtype=out_dtype, device=x.device)
     s = torch.empty((M, 1), dtype=torch.float32, device=x.device) if return_scale else None
     ldx = x.stride(0) if M > 1 else K
@@ -199,6 +207,61 @@ def quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
         return False
     cfg = _cconfig(config) if isinstance(config, Config) else None
     return _lib.lib().i8l_w8a8_mm_dynq_supported(m, n, k, cfg) == _lib.OK
+
+
+# Largest M that silu_mul_quant_mm takes.  Every column tile reads and computes the
+# SiLU-and-mul of its token rows (2K values a row), so the folded launch pays off only for
+# very few tokens: measured in the 28-layer Qwen3-1.7B stand-in on MI355X (graph replay),
+# 26.45 against 28.57 us a layer at M = 1, 28.22 against 28.80 at M = 2, but 32.15 against
+# 29.36 at M = 4 and 40.02 against 31.08 at M = 8 (the kernel itself takes up to 8 rows).
+SILU_MM_MAX_M = 2
+
+
+def silu_mul_quant_mm(gate_up: torch.Tensor, b_q: torch.Tensor, scale_b: torch.Tensor,
+                      out_dtype: torch.dtype = torch.bfloat16, bias: torch.Tensor | None = None,
+                      precise_div: bool = True, round_silu: bool = False, *, config=None,
+                      return_scale: bool = False):
+    """silu_mul_quant(gate_up) followed by w8a8_mm, as one kernel, for up to SILU_MM_MAX_M
+    tokens: the MLP's down projection fed straight from gate_up_proj's output.
+
+    Bit for bit w8a8_mm(*silu_mul_quant(gate_up, precise_div, round_silu), b_q, ..., scale_b,
+    out_dtype, bias) (reference fused_quant.py:76-88 and kernel.py:202-257 in one launch).
+    gate_up is bf16/fp16 [M, 2K] with unit column stride, the gate values first; b_q the
+    K-contiguous [K, N] view of the down weight.  Raises NotSupported for more tokens, a K no
+    built tile takes, or layouts the fused kernel does not read (make the two calls then).
+    """
+    from int8_linear.kernel import Config, _cconfig
+    if gate_up.dim() != 2 or b_q.dim() != 2 or gate_up.shape[1] != 2 * b_q.shape[0]:
+        raise ValueError(f"gate_up {tuple(gate_up.shape)} does not feed b_q {tuple(b_q.shape)}")
+    act = _act_code(gate_up, "gate_up")
+    M, K = gate_up.shape[0], b_q.shape[0]
+    if M > SILU_MM_MAX_M:
+        raise NotSupported(f"silu_mul_quant_mm takes up to {SILU_MM_MAX_M} tokens, got {M}")
+    if gate_up.stride(1) != 1:
+        raise NotSupported("gate_up needs a unit column stride")
+    N, sb, bias, bias_code, out_code = _mm_operands(gate_up, b_q, scale_b, bias, out_dtype,
+                                                    "silu_mul_quant_mm")
+    out = torch.empty((M, N), dtype=out_dtype, device=gate_up.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=gate_up.device) if return_scale else None
+    ldgu = gate_up.stride(0) if M > 1 else 2 * K
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    status = _lib.lib().i8l_silu_mul_quant_mm(
+        gate_up.data_ptr(), ldgu, act, int(bool(round_silu)), int(bool(precise_div)),
+        b_q.data_ptr(), b_q.stride(0), b_q.stride(1), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
+        out.stride(0), out_code, s.data_ptr() if s is not None else None, M, N, K, cfg,
+        _lib.stream_of(gate_up))
+    _lib.check(status, NotSupported)
+    return (out, s) if return_scale else out
+
+
+def silu_mul_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
+    """Whether silu_mul_quant_mm takes M tokens of gate_up [M, 2K] into an [N, K] weight."""
+    from int8_linear.kernel import Config, _cconfig
+    if m > SILU_MM_MAX_M:
+        return False
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    return _lib.lib().i8l_silu_mul_quant_mm_supported(m, n, k, cfg) == _lib.OK
 
 
 # Numerics the custom ops use (reference fused_quant.py:127-129 defaults);

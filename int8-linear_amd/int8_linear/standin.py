@@ -16,7 +16,9 @@ The reference slices the q columns with .contiguous() and then quantizes them
 (bench/fuse_quant.py:233-234). Here the per-token quantizer reads the slice in place, so
 each layer issues 8 kernels instead of 9, and the values are the same.  Up to
 fused_quant.QUANT_MM_MAX_M tokens, the quantizer and o_proj are one kernel
-(fused_quant.quant_mm), which again gives the same bits: 7 kernels a layer.
+(fused_quant.quant_mm), and for the few tokens fused_quant.silu_mul_quant_mm takes,
+SiLU-and-mul+quant and down_proj are one kernel too; each gives the same bits as the two
+kernels it replaces: 6 kernels a layer at 1 token.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
@@ -54,6 +56,8 @@ class DecoderStandIn:
         self.m = m
         # per-linear configurations ({name: Config}); a linear not named takes choose_config
         self.configs: dict = {}
+        # fold silu_mul_quant into down_proj where the library takes it (fused_down)
+        self.use_fused_down = True
         self.x = torch.randn((m, HIDDEN), generator=g, device=generator_device).to(
             torch.bfloat16).to(dev)
         self.norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
@@ -82,6 +86,12 @@ class DecoderStandIn:
         """Whether o_proj takes its input unquantized (quantizer folded into the GEMM)."""
         return fq.quant_mm_supported(self.m, HIDDEN, Q_COLS)
 
+    @property
+    def fused_down(self) -> bool:
+        """Whether down_proj takes gate_up's output directly (SiLU-and-mul and its quantizer
+        folded into the GEMM), for few tokens; otherwise silu_mul_quant runs on its own."""
+        return self.use_fused_down and fq.silu_mul_quant_mm_supported(self.m, HIDDEN, INTER)
+
     def weight_bytes(self) -> int:
         return sum(w.numel() + 4 * s.numel() for layer in self.layers for w, s in layer.values())
 
@@ -92,7 +102,7 @@ class DecoderStandIn:
     def forward(self, with_residual: bool = False):
         """One step through every layer; returns the last down_proj output [m, HIDDEN] (and
         the residual stream entering the last layer's MLP norm, with_residual=True)."""
-        fused_o = self.fused_o
+        fused_o, fused_down = self.fused_o, self.fused_down
         res = self.x
         q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
         h = None
@@ -108,8 +118,13 @@ class DecoderStandIn:
                 h = self.mm(layer, "o_proj", q, s)
             q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
             gu = self.mm(layer, "gate_up_proj", q, s)
-            q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)
-            h = self.mm(layer, "down_proj", q, s)
+            if fused_down:
+                w, ws = layer["down_proj"]
+                h = fq.silu_mul_quant_mm(gu, w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV,
+                                         fq.ROUND_SILU)
+            else:
+                q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)
+                h = self.mm(layer, "down_proj", q, s)
         return (h, res) if with_residual else h
 
 
