@@ -47,14 +47,17 @@ enum {
  *   bm, bn, bk : output rows (tokens) x output columns x K bytes per workgroup step
  *   warps      : wavefronts (64 lanes) per workgroup
  *   stages     : the schedule: 1 weights streamed into registers (decode); 3 with bm <= 128
- *                and bn <= 32 weights through LDS (decode); 4 with bn <= 32 the same in one
+ *                and bn <= 64 weights through LDS (decode); 4 with bn <= 32 the same in one
  *                K step a wave, each workgroup walking several column tiles with the
- *                activations held in registers (decode, K == bk * warps); 2 LDS staged
- *                through registers, 3..8 a ring of that many direct-to-LDS buffers, >= 10 a
- *                ring of stages - 8 buffers (2: a double buffer) with fragment reads
+ *                activations held in registers (decode, K == bk * warps); 5 the stages-3
+ *                tile with K split over group_m workgroups and their int32 partials summed
+ *                by a second kernel (decode; needs a workspace, see i8l_w8a8_mm_ws); 2 LDS
+ *                staged through registers, 3..8 a ring of that many direct-to-LDS buffers,
+ *                >= 10 a ring of stages - 8 buffers (2: a double buffer) with fragment reads
  *                overlapped with the MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); with
- *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4)
+ *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4); with
+ *                stages 5, the parts K is split into (2, 4 or 8)
  * A config the library was not built for returns I8L_UNSUPPORTED.
  */
 typedef struct i8l_config {
@@ -75,6 +78,9 @@ typedef struct i8l_config {
  * row stride stride_cm and unit column stride, of out_dtype bf16/f16/f32/i32.
  * cfg NULL picks the library default for (M,N,K).
  *
+ * A config that splits K (stages 5) needs a workspace: this entry declines it with
+ * I8L_UNSUPPORTED; i8l_w8a8_mm_ws takes it.
+ *
  * Replaces the reference's launch of the Triton kernel _w8a8_mm from
  * w8a8_mm (int8_linear/kernel.py:202-257; kernel body 63-124).
  */
@@ -86,6 +92,34 @@ int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak,
                 void* out, int64_t stride_cm, int32_t out_dtype,
                 int64_t M, int64_t N, int64_t K,
                 const i8l_config* cfg, void* stream);
+
+/*
+ * Bytes of device workspace that i8l_w8a8_mm_ws needs for (M,N,K,cfg): group_m * M * N * 4
+ * for a split of K (stages 5: one int32 partial plane per part), 0 for every other
+ * schedule and for cfg NULL (the default config never splits).  Host-only; always >= 0.
+ * Replaces nothing in the reference (its Triton kernel keeps the whole K loop in one
+ * program, int8_linear/kernel.py:94-103); it sizes the buffer the caller allocates.
+ */
+int64_t i8l_w8a8_mm_workspace_bytes(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
+
+/*
+ * i8l_w8a8_mm with a caller-allocated device workspace of workspace_bytes bytes, 16-byte
+ * aligned (NULL and 0 when i8l_w8a8_mm_workspace_bytes is 0).  Only a split of K uses it:
+ * the first kernel writes every byte it later reads, so the contents on entry do not
+ * matter, and on return they are undefined.  Calls in flight at the same time must not
+ * share a workspace.  A workspace smaller than needed returns I8L_INVALID_ARG.
+ * Replaces the same reference launch as i8l_w8a8_mm (int8_linear/kernel.py:202-257), with
+ * the kernel's K loop (kernel.py:94-103) split across workgroups for stages 5.
+ */
+int i8l_w8a8_mm_ws(const int8_t* a, int64_t stride_am, int64_t stride_ak,
+                   const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                   const float* scale_a, int64_t scale_a_len,
+                   const float* scale_b, int64_t scale_b_len,
+                   const void* bias, int32_t bias_dtype,
+                   void* out, int64_t stride_cm, int32_t out_dtype,
+                   int64_t M, int64_t N, int64_t K,
+                   void* workspace, int64_t workspace_bytes,
+                   const i8l_config* cfg, void* stream);
 
 /*
  * Whether i8l_w8a8_mm takes this (M,N,K,cfg) on a fast schedule: returns I8L_OK or

@@ -188,7 +188,10 @@ __host__ __device__ constexpr int stream_max_threads(int mt, int nt) {
 }
 
 // Weights-through-LDS decode tiles: the largest workgroup (threads) of a tile.
-__host__ __device__ constexpr int wlds_bound(int mt, int ks) { return mt * ks <= 6 ? 1024 : 512; }
+// 64-column tiles hold twice the weight fragments and accumulators, so they count double.
+__host__ __device__ constexpr int wlds_bound(int mt, int ks, int nc = 16) {
+  return mt * ks * (nc > 32 ? 2 : 1) <= 6 ? 1024 : 512;
+}
 // Whether the multi-step kernel's registers fit: two sets of activation fragments, the
 // weight fragments of a step and the accumulators, in VGPRs (64 x 4 bytes each).
 __host__ __device__ constexpr bool wlds_multi_fits(int mt, int nc, int ks) {
@@ -235,6 +238,11 @@ inline void lds_opt_in(const void* kern, size_t bytes, std::atomic<uint64_t>& do
 // Decode (i8l_gemm_decode.hip).
 bool stream_ok(const i8l_config& c);
 bool wlds_ok(const i8l_config& c, int64_t K);
+bool wlds_split_ok(const i8l_config& c, int64_t K);
+int64_t wlds_split_workspace(const i8l_config& c, int64_t M, int64_t N);
+hipError_t launch_wlds_split(const i8l_config& c, const int8_t* a, int64_t lda,
+                             const int8_t* b, int64_t ldb, const Epi& e, int64_t K,
+                             int32_t* ws, hipStream_t st);
 hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int K, hipStream_t st);
 hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,

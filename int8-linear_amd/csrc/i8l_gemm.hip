@@ -147,7 +147,7 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
     return I8L_UNSUPPORTED;
   }
   if (!stream_ok(c) && staged_index(c) < 0 && dma_index(c) < 0 && dmap_index(c) < 0 &&
-      !wlds_ok(c, K) && !wldsp_ok(c, K)) {
+      !wlds_ok(c, K) && !wldsp_ok(c, K) && !wlds_split_ok(c, K)) {
     set_error("config %dx%dx%d w%d s%d g%d is not built into this library", c.bm, c.bn,
               c.bk, c.warps, c.stages, c.group_m);
     return I8L_UNSUPPORTED;
@@ -159,12 +159,22 @@ extern "C" int i8l_w8a8_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_
   return I8L_OK;
 }
 
-extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak, const int8_t* b,
-                           int64_t stride_bk, int64_t stride_bn, const float* scale_a,
-                           int64_t scale_a_len, const float* scale_b, int64_t scale_b_len,
-                           const void* bias, int32_t bias_dtype, void* out, int64_t stride_cm,
-                           int32_t out_dtype, int64_t M, int64_t N, int64_t K,
-                           const i8l_config* cfg, void* stream) {
+extern "C" int64_t i8l_w8a8_mm_workspace_bytes(int64_t M, int64_t N, int64_t K,
+                                               const i8l_config* cfg) {
+  if (!cfg || M <= 0 || N <= 0 || !wlds_split_ok(*cfg, K)) return 0;
+  return wlds_split_workspace(*cfg, M, N);
+}
+
+namespace i8l {
+
+// The GEMM behind every entry point: validation, then the schedule of the config.  `ws` is
+// the split of K's workspace (NULL, 0 when the caller has none).
+int w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak, const int8_t* b,
+            int64_t stride_bk, int64_t stride_bn, const float* scale_a, int64_t scale_a_len,
+            const float* scale_b, int64_t scale_b_len, const void* bias, int32_t bias_dtype,
+            void* out, int64_t stride_cm, int32_t out_dtype, int64_t M, int64_t N, int64_t K,
+            void* ws, int64_t ws_bytes, const i8l_config* cfg, void* stream,
+            const char* who) {
   if (M < 0 || N < 0 || K < 0) {
     set_error("negative size M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
     return I8L_INVALID_ARG;
@@ -223,26 +233,38 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
                     (stride_cm * osz) % 16 == 0 && stride_cm >= N && N % 4 == 0 &&
                     (e.sb_per_col == 0 || aligned16(scale_b)) &&
                     (e.bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
+  // the weights-through-LDS schedules keep in-tile row offsets (< 128 token rows, < 64
+  // weight rows) in 32 bits; larger strides take the generic kernel
+  const bool wlds = c.stages >= 3 && c.stages <= 5 && c.bn <= 64;
+  const bool small_strides = stride_am <= INT32_MAX / 128 && stride_bn <= INT32_MAX / 64;
+  if (fast && wlds && small_strides && c.stages == 5) {
+    const int64_t need = wlds_split_workspace(c, M, N);
+    if (!ws) {
+      set_error("%s: config %dx%dx%d w%d s%d g%d splits K and needs a %lld-byte workspace "
+                "(i8l_w8a8_mm_ws)", who, c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m,
+                (long long)need);
+      return I8L_UNSUPPORTED;
+    }
+    if (ws_bytes < need || !aligned16(ws)) {
+      set_error("%s: the workspace must be 16-byte aligned and hold %lld bytes (got %lld)",
+                who, (long long)need, (long long)ws_bytes);
+      return I8L_INVALID_ARG;
+    }
+  }
   hipError_t err;
-  if (!fast) {
+  if (!fast || (wlds && !small_strides)) {
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
     hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
                        stride_bk, stride_bn, e, K);
     err = hipGetLastError();
   } else if (c.stages == 1) {
     err = launch_stream(c, a, stride_am, b, stride_bn, e, (int)K, hs);
-  } else if ((c.stages == 3 || c.stages == 4) && c.bn <= 32) {
-    // the schedules keep in-tile row offsets (< 128 token rows, < 32 weight rows) in 32 bits
-    if (stride_am > INT32_MAX / 128 || stride_bn > INT32_MAX / 32) {
-      const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
-      hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
-                         stride_bk, stride_bn, e, K);
-      err = hipGetLastError();
-    } else if (c.stages == 4) {
-      err = launch_wldsp(c, a, stride_am, b, stride_bn, e, hs);
-    } else {
-      err = launch_wlds(c, a, stride_am, b, stride_bn, e, K, hs);
-    }
+  } else if (wlds && c.stages == 5) {
+    err = launch_wlds_split(c, a, stride_am, b, stride_bn, e, K, (int32_t*)ws, hs);
+  } else if (wlds && c.stages == 4) {
+    err = launch_wldsp(c, a, stride_am, b, stride_bn, e, hs);
+  } else if (wlds && c.stages == 3) {
+    err = launch_wlds(c, a, stride_am, b, stride_bn, e, K, hs);
   } else if (c.stages == 2) {
     err = launch_staged(staged_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   } else if (c.stages >= 2 + kPipelined) {
@@ -250,7 +272,32 @@ extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak
   } else {
     err = launch_dma(dma_index(c), c, a, stride_am, b, stride_bn, e, (int)K, hs);
   }
-  return hip_status(err, "i8l_w8a8_mm launch");
+  return hip_status(err, who);
+}
+
+}  // namespace i8l
+
+extern "C" int i8l_w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak, const int8_t* b,
+                           int64_t stride_bk, int64_t stride_bn, const float* scale_a,
+                           int64_t scale_a_len, const float* scale_b, int64_t scale_b_len,
+                           const void* bias, int32_t bias_dtype, void* out, int64_t stride_cm,
+                           int32_t out_dtype, int64_t M, int64_t N, int64_t K,
+                           const i8l_config* cfg, void* stream) {
+  return w8a8_mm(a, stride_am, stride_ak, b, stride_bk, stride_bn, scale_a, scale_a_len,
+                 scale_b, scale_b_len, bias, bias_dtype, out, stride_cm, out_dtype, M, N, K,
+                 nullptr, 0, cfg, stream, "i8l_w8a8_mm");
+}
+
+extern "C" int i8l_w8a8_mm_ws(const int8_t* a, int64_t stride_am, int64_t stride_ak,
+                              const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                              const float* scale_a, int64_t scale_a_len, const float* scale_b,
+                              int64_t scale_b_len, const void* bias, int32_t bias_dtype,
+                              void* out, int64_t stride_cm, int32_t out_dtype, int64_t M,
+                              int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                              const i8l_config* cfg, void* stream) {
+  return w8a8_mm(a, stride_am, stride_ak, b, stride_bk, stride_bn, scale_a, scale_a_len,
+                 scale_b, scale_b_len, bias, bias_dtype, out, stride_cm, out_dtype, M, N, K,
+                 workspace, workspace_bytes, cfg, stream, "i8l_w8a8_mm_ws");
 }
 
 extern "C" int i8l_w8a8_mm_dynq_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg) {

@@ -137,8 +137,8 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 }
 
 // ------------------------------------------------------------------ weights-through-LDS schedule
-// Decode tile of 16*MT tokens x NC columns (NC = 16, 8 or 4).  Each wave owns one contiguous
-// K slice of `steps` steps of S = 64*KS bytes.  Per step it copies its NC x S weight bytes
+// Decode tile of 16*MT tokens x NC columns (NC = 64, 32, 16, 8 or 4).  Each wave owns one
+// contiguous K slice of `steps` steps of S = 64*KS bytes.  Per step it copies its NC x S weight bytes
 // into its own LDS buffer with global_load_lds_dwordx4: one instruction moves 1 KiB, whole
 // row segments of S bytes, so HBM sees full cache lines (the MFMA operand layout would read
 // 16 rows x 64 bytes per instruction instead).  LDS row r holds 16-byte chunk c at slot
@@ -148,6 +148,10 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // synchronisation until the cross-wave sum of the int32 partials.
 // With NC < 16, MFMA rows i and i+NC read the same weight row and only rows below NC are
 // stored.  Token rows past M read row 0 and are never stored.
+// Split of K across workgroups: with gridDim.z = Z > 1, workgroup z takes the z-th of Z equal
+// parts of K (W * steps * S bytes each) and stores its exact int32 partial tile into plane z
+// of an [Z][M][ldc] int32 buffer (the Epi's output, raw); splitk_sum adds the planes and
+// applies the epilogue.
 
 // s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
 // no LDS read of the DMA'd data is scheduled above the wait.
@@ -161,7 +165,7 @@ __device__ __forceinline__ void wait_vmcnt_wlds() {
 typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 
 template <int MT, int NC, int KS, int EK>
-__global__ void __launch_bounds__(wlds_bound(MT, KS))
+__global__ void __launch_bounds__(wlds_bound(MT, KS, NC))
 gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
           Epi e, int steps, int nbuf) {
   constexpr int S = 64 * KS;                 // K bytes per row per step
@@ -189,7 +193,8 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
-  const int64_t kw = (int64_t)wave * steps * S;
+  const int64_t kw = (int64_t)(blockIdx.z * W + wave) * steps * S;
+  if (gridDim.z > 1) e.out = (int32_t*)e.out + (int64_t)blockIdx.z * e.M * e.ldc;
   int8_t* wbuf = lds + (size_t)wave * nbuf * SB;
 
   // DMA sources of this lane: instruction t writes LDS bytes [t*1024, t*1024+1024) of the
@@ -808,7 +813,8 @@ constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1
                               {2, 16, 2}, {2, 16, 4}, {2, 8, 2},  {2, 8, 4},  {4, 16, 2},
                               {4, 16, 4}, {4, 8, 2},  {4, 8, 4},  {8, 16, 2}, {8, 8, 2},
                               {1, 32, 2}, {1, 32, 4}, {2, 32, 2}, {2, 32, 4}, {4, 32, 2},
-                              {4, 32, 4}};
+                              {4, 32, 4}, {1, 64, 2}, {2, 64, 2}, {4, 64, 2}, {1, 64, 4},
+                              {2, 64, 4}};
 
 size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
   const int64_t steps = K / ((int64_t)c.bk * c.warps);
@@ -820,11 +826,11 @@ size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
 bool wlds1_built(int mt, int nc, int W, int ks);
 
 bool wlds_ok(const i8l_config& c, int64_t K) {
-  if (c.stages != 3 || c.bn > 32 || c.warps < 1 || c.warps > 16) return false;
+  if (c.stages != 3 || c.bn > 64 || c.warps < 1 || c.warps > 16) return false;
   bool built = false;
   for (auto t : kWlds)
     if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
-        c.warps * 64 <= wlds_bound(t.mt, t.ks))
+        c.warps * 64 <= wlds_bound(t.mt, t.ks, t.nc))
       built = true;
   if (!built || K <= 0 || K % ((int64_t)c.bk * c.warps)) return false;
   const bool one_step = K == (int64_t)c.bk * c.warps &&
@@ -931,7 +937,120 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
   I8L_WLDS(8, 16, 2) I8L_WLDS(8, 8, 2)
   I8L_WLDS(1, 32, 2) I8L_WLDS(1, 32, 4) I8L_WLDS(2, 32, 2) I8L_WLDS(2, 32, 4)
   I8L_WLDS(4, 32, 2) I8L_WLDS(4, 32, 4)
+  I8L_WLDS(1, 64, 2) I8L_WLDS(2, 64, 2) I8L_WLDS(4, 64, 2) I8L_WLDS(1, 64, 4) I8L_WLDS(2, 64, 4)
 #undef I8L_WLDS
+  return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------ split of K across workgroups
+// stages 5: the weights-through-LDS tile (bm, bn, bk, warps as for stages 3) with K cut into
+// group_m equal parts, one workgroup each (grid z), so that wide tiles still give every CU
+// work.  Pass 1 is gemm_wlds writing exact int32 partial tiles into planes of a workspace;
+// pass 2 (splitk_sum) adds the planes, in plane order (int32 addition is exact, so the sum is
+// the unsplit accumulator bit for bit), and applies the same epilogue as every other
+// schedule.  A tile's L2-to-CU traffic is (bm + bn) bytes per K byte, so at 32-128 tokens a
+// 64x64 tile moves half of what 32x32 tiles do; the split restores the workgroup count the
+// wide tile gives up.
+
+// One thread per 4 consecutive output columns of one row.
+template <int Z, int EK>
+__global__ void __launch_bounds__(256)
+splitk_sum(const int32_t* __restrict__ ws, Epi e) {
+  const int nq = e.N >> 2;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= (int64_t)e.M * nq) return;
+  const int64_t m = q / nq, n = (q - m * nq) * 4;
+  const int64_t plane = (int64_t)e.M * e.N;
+  const int32_t* p = ws + m * e.N + n;
+  v4i part[Z];
+#pragma unroll
+  for (int z = 0; z < Z; ++z) part[z] = *(const v4i*)(p + z * plane);
+  v4i sum = part[0];
+#pragma unroll
+  for (int z = 1; z < Z; ++z) sum += part[z];
+  store4<EK>(e, m, n, sum);
+}
+
+int64_t wlds_split_workspace(const i8l_config& c, int64_t M, int64_t N) {
+  return c.stages == 5 ? (int64_t)c.group_m * M * N * 4 : 0;
+}
+
+bool wlds_split_ok(const i8l_config& c, int64_t K) {
+  if (c.stages != 5 || (c.group_m != 2 && c.group_m != 4 && c.group_m != 8)) return false;
+  if (c.bn > 64 || c.warps < 1 || c.warps > 16 || c.bk <= 0) return false;
+  bool built = false;
+  for (auto t : kWlds)
+    if (16 * t.mt == c.bm && t.nc == c.bn && 64 * t.ks == c.bk &&
+        c.warps * 64 <= wlds_bound(t.mt, t.ks, t.nc) && wlds_multi_fits(t.mt, t.nc, t.ks))
+      built = true;
+  const int64_t part = (int64_t)c.bk * c.warps * c.group_m;
+  if (!built || K <= 0 || K % part) return false;
+  return wlds_lds_bytes(c, K / c.group_m) <= kMaxLds;
+}
+
+template <int Z>
+hipError_t launch_splitk_sum(const int32_t* ws, const Epi& e, hipStream_t st) {
+  const int64_t quads = (int64_t)e.M * (e.N / 4);
+  const dim3 grid((unsigned)((quads + 255) / 256));
+  switch (epi_kind(e)) {
+    case EK_BF16: hipLaunchKernelGGL((splitk_sum<Z, EK_BF16>), grid, dim3(256), 0, st, ws, e); break;
+    case EK_BF16_BBF16:
+      hipLaunchKernelGGL((splitk_sum<Z, EK_BF16_BBF16>), grid, dim3(256), 0, st, ws, e);
+      break;
+    default: hipLaunchKernelGGL((splitk_sum<Z, EK_ANY>), grid, dim3(256), 0, st, ws, e);
+  }
+  return hipGetLastError();
+}
+
+template <int MT, int NC, int KS>
+hipError_t launch_wlds_part(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                            int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
+  if constexpr (wlds_multi_fits(MT, NC, KS)) {
+    auto kern = gemm_wlds<MT, NC, KS, EK_ANY>;
+    const int64_t kpart = K / c.group_m;
+    const size_t shm = wlds_lds_bytes(c, kpart);
+    static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+    lds_opt_in((const void*)kern, kMaxLds, lds_done);
+    const int steps = (int)(kpart / ((int64_t)c.bk * c.warps));
+    const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT), c.group_m);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
+                       steps > 1 ? 2 : 1);
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_wlds_split(const i8l_config& c, const int8_t* a, int64_t lda,
+                             const int8_t* b, int64_t ldb, const Epi& e, int64_t K,
+                             int32_t* ws, hipStream_t st) {
+  Epi part = e;  // pass 1: raw int32 planes, ldc = N
+  part.out = ws;
+  part.ldc = e.N;
+  part.out_dtype = I8L_I32;
+  part.bias = nullptr;
+  part.bias_dtype = I8L_DTYPE_NONE;
+  part.sa_per_row = part.sb_per_col = 0;
+  const int mt = c.bm / 16, nc = c.bn, ks = c.bk / 64;
+  hipError_t err = hipErrorInvalidValue;
+#define I8L_WLDS(MT_, NC_, KS_)                                                             \
+  if (mt == MT_ && nc == NC_ && ks == KS_) err = launch_wlds_part<MT_, NC_, KS_>(c, a, lda, b, ldb, part, K, st); else
+  I8L_WLDS(1, 16, 2) I8L_WLDS(1, 16, 4) I8L_WLDS(1, 16, 6) I8L_WLDS(1, 16, 8)
+  I8L_WLDS(1, 8, 2) I8L_WLDS(1, 8, 4) I8L_WLDS(1, 8, 6) I8L_WLDS(1, 8, 8)
+  I8L_WLDS(1, 4, 4) I8L_WLDS(1, 4, 8)
+  I8L_WLDS(2, 16, 2) I8L_WLDS(2, 16, 4) I8L_WLDS(2, 8, 2) I8L_WLDS(2, 8, 4)
+  I8L_WLDS(4, 16, 2) I8L_WLDS(4, 16, 4) I8L_WLDS(4, 8, 2) I8L_WLDS(4, 8, 4)
+  I8L_WLDS(8, 16, 2) I8L_WLDS(8, 8, 2)
+  I8L_WLDS(1, 32, 2) I8L_WLDS(1, 32, 4) I8L_WLDS(2, 32, 2) I8L_WLDS(2, 32, 4)
+  I8L_WLDS(4, 32, 2) I8L_WLDS(4, 32, 4)
+  I8L_WLDS(1, 64, 2) I8L_WLDS(2, 64, 2) I8L_WLDS(4, 64, 2) I8L_WLDS(1, 64, 4) I8L_WLDS(2, 64, 4)
+  {}
+#undef I8L_WLDS
+  if (err != hipSuccess) return err;
+  switch (c.group_m) {
+    case 2: return launch_splitk_sum<2>(ws, e, st);
+    case 4: return launch_splitk_sum<4>(ws, e, st);
+    case 8: return launch_splitk_sum<8>(ws, e, st);
+  }
   return hipErrorInvalidValue;
 }
 

@@ -130,11 +130,17 @@ py::object mm(const at::Tensor& a, const at::Tensor& b, const at::Tensor& sa,
     bias_ptr = bt.data_ptr();
   }
   at::Tensor out = at::empty({m, n}, a.options().dtype(out_dtype));
-  const int st = i8l_w8a8_mm(
+  // a split of K takes its int32 partial planes from the caching allocator (stream-ordered,
+  // and from the graph's pool under capture)
+  const int64_t ws_bytes = i8l_w8a8_mm_workspace_bytes(m, n, k, &c);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, a.options().dtype(at::kByte));
+  const int st = i8l_w8a8_mm_ws(
       (const int8_t*)a.data_ptr(), a.stride(0), a.stride(1), (const int8_t*)b.data_ptr(),
       b.stride(0), b.stride(1), (const float*)sa.data_ptr(), sa.numel(),
       (const float*)sb.data_ptr(), sb.numel(), bias_ptr, bias_code, out.data_ptr(),
-      out.stride(0), out_code, m, n, k, &c, stream_of(a));
+      out.stride(0), out_code, m, n, k, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, &c,
+      stream_of(a));
   if (st != I8L_OK) return py::none();
   ++g_launches;
   return py::cast(out);

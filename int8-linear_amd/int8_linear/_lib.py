@@ -33,8 +33,8 @@ class CConfig(ctypes.Structure):
 EXPORTS = ("i8l_w8a8_mm", "i8l_w8a8_mm_supported", "i8l_default_config",
            "i8l_add_rmsnorm_quant", "i8l_silu_mul_quant", "i8l_quant_per_token",
            "i8l_w8a8_mm_dynq", "i8l_w8a8_mm_dynq_supported",
-           "i8l_silu_mul_quant_mm", "i8l_silu_mul_quant_mm_supported",
-           "i8l_last_error", "i8l_version")
+           "i8l_silu_mul_quant_mm", "i8l_silu_mul_quant_mm_supported", "i8l_w8a8_mm_ws",
+           "i8l_w8a8_mm_workspace_bytes", "i8l_last_error", "i8l_version")
 
 _lib: ctypes.CDLL | None = None
 
@@ -65,8 +65,12 @@ def lib() -> ctypes.CDLL:
                                         _P, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64,
                                         ctypes.POINTER(CConfig), _P]
     L.i8l_silu_mul_quant_mm_supported.argtypes = [_I64, _I64, _I64, ctypes.POINTER(CConfig)]
+    L.i8l_w8a8_mm_ws.argtypes = L.i8l_w8a8_mm.argtypes[:-2] + [_P, _I64] + \
+        L.i8l_w8a8_mm.argtypes[-2:]
+    L.i8l_w8a8_mm_workspace_bytes.argtypes = [_I64, _I64, _I64, ctypes.POINTER(CConfig)]
     for name in EXPORTS[:-2]:
         getattr(L, name).restype = ctypes.c_int
+    L.i8l_w8a8_mm_workspace_bytes.restype = _I64
     L.i8l_last_error.restype = ctypes.c_char_p
     L.i8l_version.restype = ctypes.c_char_p
     _lib = L

@@ -36,13 +36,16 @@ class NotSupported(Exception):
 class Config:
     """One GEMM launch configuration (reference kernel.py:49-60), in MI355X terms.
 
-    Decode schedules (bm <= 128 tokens a workgroup, bn <= 32 columns):
+    Decode schedules (bm <= 128 tokens a workgroup, bn <= 64 columns):
       stages == 1: weights streamed into MFMA registers; `warps` waves split K in 64-byte
         steps, so bk == 64 * warps.
       stages == 3: weights copied through LDS with direct-to-LDS loads; each of the
         `warps` waves owns one K slice taken bk bytes per step (K a multiple of bk * warps).
       stages == 4: the same with one K step a wave (K == bk * warps), each workgroup walking
         several column tiles with its activations held in registers.
+      stages == 5: the stages-3 tile (up to 64 columns) with K split into group_m (2, 4 or 8)
+        parts, one workgroup each, and the int32 partials summed by a second kernel; the
+        call allocates the partials' workspace (group_m * M * N * 4 bytes).
     Prefill schedules (bm x bn macro tiles of 64 to 256, K in bk-byte steps, `group_m`
     rows of tiles walked together):
       stages == 2: double-buffered LDS staged through registers;
@@ -229,12 +232,17 @@ def w8a8_mm(
             raise NotSupported(f"output dtype {out_dtype} is not supported")
 
     out = torch.empty((m, n), dtype=torch.int32 if raw else out_dtype, device=a_q.device)
-    status = _lib.lib().i8l_w8a8_mm(
+    # A split of K writes int32 partial planes to a workspace from the caching allocator
+    # (stream-ordered, and from the graph's pool under capture).
+    ws_bytes = _lib.lib().i8l_w8a8_mm_workspace_bytes(m, n, k, _cconfig(cfg))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a_q.device) if ws_bytes else None
+    status = _lib.lib().i8l_w8a8_mm_ws(
         a_q.data_ptr(), a_q.stride(0), a_q.stride(1),
         b_q.data_ptr(), b_q.stride(0), b_q.stride(1),
         sa.data_ptr(), sa.numel(), sb.data_ptr(), sb.numel(),
         bias.data_ptr() if bias is not None else None, bias_code,
         out.data_ptr(), out.stride(0), out_code,
-        m, n, k, _cconfig(cfg), _lib.stream_of(a_q))
+        m, n, k, ws.data_ptr() if ws is not None else None, ws_bytes,
+        _cconfig(cfg), _lib.stream_of(a_q))
     _lib.check(status, NotSupported)
     return out

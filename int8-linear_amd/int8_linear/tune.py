@@ -70,7 +70,12 @@ WLDSP_TILES = [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
 WLDS_TILES = [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
               (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4),
               (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2),
-              (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4)]
+              (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4),
+              (1, 64, 2), (2, 64, 2), (4, 64, 2), (1, 64, 4), (2, 64, 4)]
+# The tiles worth splitting K for (stages 5, K in group_m parts): wide ones, whose L2-to-CU
+# traffic per output is lowest but which give fewer workgroups than there are CUs.
+SPLIT_TILES = [(1, 32, 2), (2, 32, 2), (4, 32, 2), (2, 32, 4), (1, 64, 2), (2, 64, 2),
+               (4, 64, 2), (1, 64, 4), (2, 64, 4), (8, 16, 2)]
 
 
 CAPTURE_SIZES = [1, 2, 4, *range(8, 256, 8), *range(256, 513, 16), 1024, 2048, 4096]
@@ -100,6 +105,17 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
                 cfg = Config(16 * mt, nc, 64 * ks, w, 4, g)
                 if supported(m, n, k, cfg):
                     out.append(cfg)
+        for mt, nc, ks in SPLIT_TILES:
+            tiles = -(-m // (16 * mt)) * (n // nc)
+            if mt > need or tiles >= 512:
+                continue  # enough workgroups without a split
+            for parts in (2, 4, 8):
+                if tiles * parts > 1024:
+                    continue
+                for w in (4, 8):
+                    cfg = Config(16 * mt, nc, 64 * ks, w, 5, parts)
+                    if supported(m, n, k, cfg):
+                        out.append(cfg)
     if m <= 256:
         need = next(mt for mt in (1, 2, 4, 8) if 16 * mt >= min(m, 128))
         for mt, bn in STREAM_TILES:

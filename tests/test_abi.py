@@ -98,7 +98,9 @@ def test_supported_decline_rule_matches_reference():
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 128, 4, 3, 1))     # 4 steps a wave
     assert kernel.supported(16, 4096, 2048, Config(16, 32, 128, 16, 3, 1))    # 32 columns, 1 step
     assert kernel.supported(16, 4096, 2048, Config(16, 32, 128, 8, 3, 1))     # ... or 2 steps
-    assert not kernel.supported(16, 4096, 2048, Config(16, 64, 128, 8, 3, 1))  # 64: not built
+    assert kernel.supported(16, 4096, 2048, Config(16, 64, 128, 8, 3, 1))      # 64 columns
+    assert not kernel.supported(16, 4096, 2048, Config(16, 128, 128, 8, 3, 1))  # 128: not built
+    assert not kernel.supported(16, 4096, 2048, Config(32, 64, 128, 16, 3, 1))  # would spill
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 384, 4, 3, 1))  # K % (bk*warps)
     assert not kernel.supported(16, 4096, 2048, Config(16, 16, 512, 16, 3, 1))  # LDS > 160 KiB
     assert kernel.supported(16, 4096, 2048, Config(16, 16, 64, 1, 1, 1))
@@ -107,6 +109,29 @@ def test_supported_decline_rule_matches_reference():
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 12, 8))  # overlapped ring
     assert kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 8, 4, 8))   # DMA ring of 4
     assert not kernel.supported(4096, 4096, 4096, Config(256, 256, 64, 16, 2, 8))
+
+
+def test_split_of_k_configs_and_their_workspace():
+    """stages 5 splits K into group_m parts (2, 4, 8), each a whole number of the tile's
+    bk * warps steps; the workspace is one int32 plane [M, N] a part, and only a split
+    needs one."""
+    L = _lib.lib()
+    split = Config(64, 64, 128, 4, 5, 4)
+    assert kernel.supported(128, 2048, 6144, split)
+    assert L.i8l_w8a8_mm_workspace_bytes(128, 2048, 6144, kernel._cconfig(split)) == 4 * 128 * 2048 * 4
+    assert L.i8l_w8a8_mm_workspace_bytes(100, 2048, 6144, kernel._cconfig(split)) == 4 * 100 * 2048 * 4
+    assert L.i8l_w8a8_mm_workspace_bytes(0, 2048, 6144, kernel._cconfig(split)) == 0
+    assert L.i8l_w8a8_mm_workspace_bytes(128, 2048, 6144, None) == 0          # default: no split
+    unsplit = Config(64, 64, 128, 4, 3, 1)
+    assert L.i8l_w8a8_mm_workspace_bytes(128, 2048, 6144, kernel._cconfig(unsplit)) == 0
+    assert kernel.supported(128, 2048, 6144, Config(64, 64, 128, 6, 5, 8))    # 768 bytes a part
+    assert not kernel.supported(128, 2048, 6144, Config(64, 64, 128, 4, 5, 8))  # 768 % 512
+    assert not kernel.supported(128, 2048, 6144, Config(64, 64, 128, 4, 5, 3))  # 3 parts
+    assert not kernel.supported(128, 2048, 2048, Config(64, 64, 256, 4, 5, 4))  # 512 a part < 1024
+    assert not kernel.supported(128, 2048, 6144, Config(64, 128, 128, 4, 5, 4))  # not built
+    assert kernel.supported(32, 4096, 14336, Config(32, 64, 128, 4, 5, 4))
+    assert L.i8l_w8a8_mm_workspace_bytes(
+        32, 4096, 14336, kernel._cconfig(Config(32, 64, 128, 4, 5, 4))) == 4 * 32 * 4096 * 4
 
 
 def test_supported_reports_the_reason():
@@ -202,6 +227,7 @@ def test_cpp_binding_loads_and_chooses_the_tuned_config():
 def test_cpp_binding_declines_what_the_python_path_must_handle():
     import torch
     f = _lib.fast()
+    before = f.launches()
     a = torch.zeros((2, 64), dtype=torch.int8)
     assert f.mm(a, torch.zeros((64, 16), dtype=torch.int8), torch.ones(1), torch.ones(1),
                 torch.bfloat16, None) is None                        # host tensors
@@ -209,7 +235,7 @@ def test_cpp_binding_declines_what_the_python_path_must_handle():
     assert f.add_rmsnorm_quant(x, None, torch.ones(64, dtype=torch.bfloat16), 1e-6, True) is None
     assert f.silu_mul_quant(x, True, False) is None
     assert f.quant_per_token(x, True) is None
-    assert f.launches() == 0
+    assert f.launches() == before
 
 
 def test_dynamic_quant_entry_validates_on_the_host():

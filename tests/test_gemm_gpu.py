@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from helpers import bits, ints, np_, offset_ints, say
-from int8_linear import Config, NotSupported, kernel, w8a8_mm
+from int8_linear import Config, NotSupported, _lib, kernel, w8a8_mm
 from int8_linear.operands import operands, seed_of
 from int8_linear.shapes import SHAPES
 from oracle import oracle as o
@@ -232,7 +232,8 @@ WLDS = [(mt, nc, ks) for mt, nc, ks in
         [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),
          (1, 8, 8), (1, 4, 4), (1, 4, 8), (2, 16, 2), (2, 16, 4), (2, 8, 2), (2, 8, 4),
          (4, 16, 2), (4, 16, 4), (4, 8, 2), (4, 8, 4), (8, 16, 2), (8, 8, 2),
-         (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4)]]
+         (1, 32, 2), (1, 32, 4), (2, 32, 2), (2, 32, 4), (4, 32, 2), (4, 32, 4),
+         (1, 64, 2), (2, 64, 2), (4, 64, 2), (1, 64, 4), (2, 64, 4)]]
 
 
 @pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
@@ -511,3 +512,101 @@ def test_long_prefill_offsets_pass_two_to_the_31():
     out = w8a8_mm(a, w.t(), sa, ws, torch.bfloat16, bias_d)
     ref = o.epilogue(acc, np_(sa)[rows], np_(w_s), bits(bias), o.BF16, o.BF16)
     assert np.array_equal(bits(out[idx]), ref)
+
+
+# The split of K across workgroups (stages 5): tiles up to 64 columns with K in 2, 4 and 8
+# parts of one or two steps a wave, ragged M; the int32 product exact, then every output
+# dtype, bias dtype and scale layout through the sum kernel's epilogue.
+SPLIT_TILES = [(1, 16, 2), (2, 32, 2), (4, 32, 2), (8, 16, 2), (1, 64, 2), (2, 64, 2),
+               (4, 64, 2), (2, 64, 4)]
+
+
+@pytest.mark.parametrize("tile", SPLIT_TILES, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
+@pytest.mark.parametrize("parts", [2, 4, 8])
+def test_split_of_k_is_exact(tile, parts):
+    mt, nc, ks = tile
+    waves, n = 4, 512
+    for steps in (1, 2):
+        k = 64 * ks * waves * steps * parts
+        cfg = Config(16 * mt, nc, 64 * ks, waves, 5, parts)
+        assert kernel.supported(16 * mt, n, k, cfg), cfg.name
+        for m in sorted({1, 16 * mt - 3, 16 * mt}):
+            say(f"w8a8_mm split m={m} k={k} n={n} config={cfg.name}")
+            a, w = ints((m, k), 21 + m), ints((n, k), 22 + steps)
+            one = torch.ones(1, device="cuda")
+            acc = o.gemm_i32(np_(a), np_(w))
+            assert np.array_equal(np_(w8a8_mm(a, w.t(), one, one, raw=True, config=cfg)), acc)
+            g = torch.Generator().manual_seed(m + parts)
+            sa = (torch.rand((m, 1), generator=g) * 1e-2 + 1e-3).cuda()
+            sb = (torch.rand((n, 1), generator=g) * 1e-2 + 1e-3).cuda()
+            for dtype, bias in ((torch.bfloat16, None),
+                                (torch.bfloat16, torch.randn(n, generator=g).to(torch.bfloat16)),
+                                (torch.float16, torch.randn(n, generator=g).to(torch.float16)),
+                                (torch.float32, torch.randn(n, generator=g))):
+                bias = bias.cuda() if bias is not None else None
+                out = w8a8_mm(a, w.t(), sa, sb, dtype, bias, config=cfg)
+                assert np.array_equal(as_np(out), oracle_out(a, w, sa, sb, bias, dtype)), \
+                    (dtype, bias is not None)
+            sb1 = sb[:1].reshape(1)
+            out = w8a8_mm(a, w.t(), sa, sb1, torch.bfloat16, config=cfg)   # scalar scale_b
+            assert np.array_equal(bits(out), oracle_out(a, w, sa, sb1, None, torch.bfloat16))
+
+
+@pytest.mark.parametrize("m,k,n,cfg", [
+    (128, 6144, 2048, Config(64, 64, 128, 4, 5, 4)),      # Qwen3 down_proj
+    (64, 6144, 2048, Config(64, 64, 128, 6, 5, 8)),
+    (128, 14336, 4096, Config(64, 64, 128, 4, 5, 4)),     # Llama-3-8B down_proj
+    (32, 14336, 4096, Config(32, 64, 128, 4, 5, 4)),
+], ids=["qwen_down_128", "qwen_down_64", "llama_down_128", "llama_down_32"])
+def test_split_of_k_at_decode_shapes(m, k, n, cfg):
+    """The BASELINE operand distributions (x ~ N(0,1), W ~ N(0,0.02), both quantized per row)
+    with a bias, at the down_proj shapes the split is for; bit-exact against the oracle and
+    the unsplit schedule."""
+    say(f"split decode shape m={m} k={k} n={n} {cfg.name}")
+    d = operands(m, k, n, seed_of(m, k, n), with_bias=True, device="cuda")
+    got = w8a8_mm(d["a_q"], d["w_qt"], d["a_s"], d["w_s"], torch.bfloat16, d["bias"], config=cfg)
+    ref = oracle_out(d["a_q"], d["w_q"], d["a_s"], d["w_s"], d["bias"], torch.bfloat16)
+    assert np.array_equal(bits(got), ref)
+    unsplit = w8a8_mm(d["a_q"], d["w_qt"], d["a_s"], d["w_s"], torch.bfloat16, d["bias"],
+                      config=Config(cfg.bm, cfg.bn, cfg.bk, 4, 3, 1))
+    assert torch.equal(got, unsplit)
+
+
+def test_split_of_k_needs_a_workspace_and_replays_in_a_graph():
+    """The workspace-less entry declines a split (it cannot allocate), the workspace entry
+    rejects one too small; under graph capture the partial planes come from the graph's
+    pool and every replay sums the current inputs."""
+    m, k, n = 48, 4096, 1024
+    cfg = Config(32, 64, 128, 4, 5, 4)
+    a, w = ints((m, k), 3), ints((n, k), 4)
+    one = torch.ones(1, device="cuda")
+    out = torch.empty((m, n), dtype=torch.int32, device="cuda")
+    L = _lib.lib()
+    args = (a.data_ptr(), a.stride(0), 1, w.data_ptr(), 1, w.stride(0), one.data_ptr(), 1,
+            one.data_ptr(), 1, None, _lib.DTYPE_NONE, out.data_ptr(), n, _lib.I32, m, n, k)
+    c = kernel._cconfig(cfg)
+    st = L.i8l_w8a8_mm(*args, c, _lib.stream_of(a))
+    assert st == _lib.UNSUPPORTED and "workspace" in _lib.last_error()
+    need = L.i8l_w8a8_mm_workspace_bytes(m, n, k, c)
+    assert need == 4 * m * n * 4
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    assert L.i8l_w8a8_mm_ws(*args, ws.data_ptr(), need - 16, c, _lib.stream_of(a)) == _lib.INVALID_ARG
+    assert L.i8l_w8a8_mm_ws(*args, ws.data_ptr(), need, c, _lib.stream_of(a)) == _lib.OK
+    torch.cuda.synchronize()
+    assert np.array_equal(np_(out), o.gemm_i32(np_(a), np_(w)))
+
+    sa = torch.full((m, 1), 1e-3, device="cuda")
+    sb = torch.full((n, 1), 2e-3, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=cfg)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=cfg)
+    for seed in (5, 6, 7):
+        a.copy_(ints((m, k), seed))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got), oracle_out(a, w, sa, sb, None, torch.bfloat16)), seed
