@@ -122,6 +122,24 @@ int i8l_w8a8_mm_ws(const int8_t* a, int64_t stride_am, int64_t stride_ak,
                    const i8l_config* cfg, void* stream);
 
 /*
+ * i8l_w8a8_mm for callers that cannot allocate: code under HIP graph capture, serving loops
+ * and harnesses that forbid allocation.  No counterpart in the reference (its Triton kernel
+ * needs no workspace).  Same arguments, validation and results as i8l_w8a8_mm_ws, but a
+ * split of K (stages 5) keeps its partial planes in a device array of the library itself,
+ * 16 MiB on each GPU it runs on (held until the process ends); a config that needs more
+ * (group_m * M * N * 4 bytes > 16 MiB) returns I8L_UNSUPPORTED.  No call allocates or frees
+ * memory.  All calls on one GPU share that array: calls that overlap in time on one GPU race.
+ */
+int i8l_w8a8_mm_noalloc(const int8_t* a, int64_t stride_am, int64_t stride_ak,
+                        const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                        const float* scale_a, int64_t scale_a_len,
+                        const float* scale_b, int64_t scale_b_len,
+                        const void* bias, int32_t bias_dtype,
+                        void* out, int64_t stride_cm, int32_t out_dtype,
+                        int64_t M, int64_t N, int64_t K,
+                        const i8l_config* cfg, void* stream);
+
+/*
  * Whether i8l_w8a8_mm takes this (M,N,K,cfg) on a fast schedule: returns I8L_OK or
  * I8L_UNSUPPORTED without launching anything (host-only; no GPU needed).  The decline
  * rule is the reference's: N % bn or K % bk non-zero (int8_linear/kernel.py:228-229),

@@ -490,3 +490,77 @@ extern "C" int i8l_silu_mul_quant_mm(const void* gate_up, int64_t ldgu, int32_t 
                                         scale_a_out, precise_div ? 1 : 0, (hipStream_t)stream);
   return hip_status(err, "i8l_silu_mul_quant_mm launch");
 }
+
+// ------------------------------------------------------------------ allocation-free entry
+// i8l_w8a8_mm_noalloc: i8l_w8a8_mm for callers that cannot allocate (code under HIP graph
+// capture, serving loops that forbid allocation), with the split of K's partial planes in
+// `scratch`, a device array of this library (kScratchBytes on every GPU the library runs on,
+// held until the process ends).  Every call on a GPU shares that GPU's array: calls that
+// overlap in time on one GPU race.  Nothing in it has to start at zero (the first kernel of
+// a split writes every partial the second reads), so it is never cleared.
+namespace i8l {
+
+constexpr int64_t kScratchBytes = 16ll << 20;
+static __device__ __align__(256) int32_t scratch[kScratchBytes / 4];
+
+constexpr int kScratchDevices = 64;
+static std::atomic<void*> g_scratch[kScratchDevices];
+
+// The device address of `scratch` on the GPU that runs `stream`, looked up once per device
+// with that device current (in host code the array's name stands for the symbol, not for
+// device memory).
+static int scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_status(e, "i8l_w8a8_mm_noalloc: hipStreamGetDevice");
+  if (dev < 0 || dev >= kScratchDevices) {
+    set_error("i8l_w8a8_mm_noalloc: device %d is beyond the %d this library serves", dev,
+              kScratchDevices);
+    return I8L_UNSUPPORTED;
+  }
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return hip_status(e, "i8l_w8a8_mm_noalloc: hipGetSymbolAddress");
+    if (!p) {
+      set_error("i8l_w8a8_mm_noalloc: no device address for the scratch array");
+      return I8L_HIP_ERROR;
+    }
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return I8L_OK;
+}
+
+}  // namespace i8l
+
+extern "C" int i8l_w8a8_mm_noalloc(const int8_t* a, int64_t stride_am, int64_t stride_ak,
+                                   const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                                   const float* scale_a, int64_t scale_a_len,
+                                   const float* scale_b, int64_t scale_b_len, const void* bias,
+                                   int32_t bias_dtype, void* out, int64_t stride_cm,
+                                   int32_t out_dtype, int64_t M, int64_t N, int64_t K,
+                                   const i8l_config* cfg, void* stream) {
+  const int64_t need = i8l_w8a8_mm_workspace_bytes(M, N, K, cfg);
+  if (need > kScratchBytes) {
+    set_error("i8l_w8a8_mm_noalloc: M=%lld N=%lld with %d parts of K needs %lld bytes of "
+              "workspace, beyond the %lld-byte scratch (use i8l_w8a8_mm_ws)", (long long)M,
+              (long long)N, cfg ? cfg->group_m : 1, (long long)need, (long long)kScratchBytes);
+    return I8L_UNSUPPORTED;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_address((hipStream_t)stream, &ws);
+    if (st != I8L_OK) return st;
+  }
+  return w8a8_mm(a, stride_am, stride_ak, b, stride_bk, stride_bn, scale_a, scale_a_len,
+                 scale_b, scale_b_len, bias, bias_dtype, out, stride_cm, out_dtype, M, N, K,
+                 ws, need > 0 ? kScratchBytes : 0, cfg, stream, "i8l_w8a8_mm_noalloc");
+}

@@ -1,0 +1,84 @@
+"""The allocation-free GEMM entry (i8l_w8a8_mm_noalloc) on the GPU, through the C ABI: a
+split of K with its partial planes in the library's own device array gives the workspace
+entry's output (i8l_w8a8_mm_ws, the caller's workspace) bit for bit, and through it the CPU
+oracle's, on two calls in a row, the second with fewer tokens; a config that needs more
+than the array holds is declined with an error, and a config without a split runs too.
+
+The entry has no counterpart in the reference: it exists for callers that cannot allocate."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, ints, np_, say
+from int8_linear import Config, _lib, kernel
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+SCRATCH_BYTES = 16 << 20
+
+
+def _call(entry, a, w, sa, sb, bias, out, out_code, cfg, ws=None):
+    m, k = a.shape
+    n = w.shape[0]
+    args = [a.data_ptr(), a.stride(0), 1, w.data_ptr(), 1, w.stride(0),
+            sa.data_ptr(), sa.numel(), sb.data_ptr(), sb.numel(),
+            bias.data_ptr() if bias is not None else None,
+            _lib.BF16 if bias is not None else _lib.DTYPE_NONE,
+            out.data_ptr(), out.stride(0), out_code, m, n, k]
+    if ws is not None:
+        args += [ws.data_ptr(), ws.numel()]
+    return entry(*args, ctypes.byref(kernel._cconfig(cfg)) if cfg else None, _lib.stream_of(a))
+
+
+def test_noalloc_equals_the_workspace_entry_twice():
+    L = _lib.lib()
+    k, n = 14336, 4096
+    cfg = Config(64, 64, 128, 4, 5, 4)
+    w = ints((n, k), 91)
+    g = torch.Generator().manual_seed(92)
+    sb = (torch.rand((n,), generator=g) * 1e-3 + 1e-4).cuda()
+    bias = torch.randn(n, generator=g).to(torch.bfloat16).cuda()
+    for m in (128, 37):                       # the second call smaller than the first
+        say(f"noalloc m={m} k={k} n={n} {cfg.name}")
+        a = ints((m, k), 93 + m)
+        sa = (torch.rand((m,), generator=g) * 1e-2 + 1e-3).cuda()
+        need = L.i8l_w8a8_mm_workspace_bytes(m, n, k, ctypes.byref(kernel._cconfig(cfg)))
+        assert 0 < need <= SCRATCH_BYTES
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        ref = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        assert _call(L.i8l_w8a8_mm_ws, a, w, sa, sb, bias, ref, _lib.BF16, cfg, ws) == _lib.OK
+        assert _call(L.i8l_w8a8_mm_noalloc, a, w, sa, sb, bias, got, _lib.BF16, cfg) == _lib.OK, \
+            _lib.last_error()
+        raw = torch.empty((m, n), dtype=torch.int32, device="cuda")
+        assert _call(L.i8l_w8a8_mm_noalloc, a, w, sa, sb, None, raw, _lib.I32, cfg) == _lib.OK
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+        acc = o.gemm_i32(np_(a), np_(w))
+        assert np.array_equal(np_(raw), acc)
+        assert np.array_equal(bits(got), o.epilogue(acc, np_(sa), np_(sb), bits(bias), o.BF16,
+                                                    o.BF16))
+
+
+def test_noalloc_declines_beyond_its_scratch_and_runs_unsplit_configs():
+    L = _lib.lib()
+    m, k, n = 128, 4096, 12288
+    cfg = Config(64, 64, 128, 4, 5, 4)         # 4 * 128 * 12288 * 4 = 24 MiB > 16 MiB
+    assert L.i8l_w8a8_mm_workspace_bytes(m, n, k, ctypes.byref(kernel._cconfig(cfg))) > SCRATCH_BYTES
+    a, w = ints((m, k), 5), ints((n, k), 6)
+    one = torch.ones(1, device="cuda")
+    out = torch.empty((m, n), dtype=torch.int32, device="cuda")
+    assert _call(L.i8l_w8a8_mm_noalloc, a, w, one, one, None, out, _lib.I32, cfg) == _lib.UNSUPPORTED
+    assert "scratch" in _lib.last_error()
+    for c in (None, Config(32, 32, 128, 4, 3, 1)):   # no split: the scratch is not used
+        say(f"noalloc unsplit {c.name if c else 'default'}")
+        out.fill_(-1)
+        assert _call(L.i8l_w8a8_mm_noalloc, a, w, one, one, None, out, _lib.I32, c) == _lib.OK
+        torch.cuda.synchronize()
+        assert np.array_equal(np_(out), o.gemm_i32(np_(a), np_(w)))
