@@ -182,7 +182,18 @@ def time_cold_us(call, copies: int, windows: int = 3) -> float:
     return statistics.median(res)
 
 
-def tune_shape(k: int, n: int, ms: list[int], device, log=print) -> dict:
+def refine_candidates(m: int, k: int, n: int) -> list[Config]:
+    """The configuration tuned_config holds now (else the default) and the schedule families
+    added after the table was made: 64-column weights-through-LDS tiles and the split of K
+    (stages 5).  Timing only these against the entry they would replace updates a table
+    without re-timing every candidate of every bucket."""
+    from int8_linear.kernel import tuned_config
+    cur = tuned_config(m, n, k) or default_config(m, n, k)
+    new = [c for c in candidate_configs(m, k, n) if c.stages == 5 or (c.stages == 3 and c.bn == 64)]
+    return [cur] + [c for c in new if c != cur]
+
+
+def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = False) -> dict:
     """{str(M): {"config": {...}, "graph_us": t, "default_us": t0}} for one weight shape."""
     d = operands(16, k, n, seed_of(16, k, n), device=device)
     copies = max(2, -(-ROTATE_BYTES // (k * n)))
@@ -196,7 +207,7 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print) -> dict:
         ref = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=default_config(m, n, k))
         t0 = None
         timed = []
-        for cfg in candidate_configs(m, k, n):
+        for cfg in (refine_candidates(m, k, n) if refine else candidate_configs(m, k, n)):
             got = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=cfg)
             if not torch.equal(got, ref):
                 raise RuntimeError(f"config {cfg.name} gives a different product at M={m} K={k} N={n}")
@@ -245,6 +256,9 @@ def main() -> int:
     ap.add_argument("--kn", default=None,
                     help="comma-separated KxN shapes of the preset to tune (default: all)")
     ap.add_argument("--merge", action="store_true", help="write the result into tuned_configs.json")
+    ap.add_argument("--refine", action="store_true",
+                    help="time only the current table entry against the newer schedule "
+                         "families (64-column tiles, split of K)")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
     dev = torch.device("cuda:0")
@@ -255,7 +269,8 @@ def main() -> int:
     for label, k, n in SHAPES[args.shapes]:
         if only is not None and f"{k}x{n}" not in only:
             continue
-        table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True))
+        table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True),
+                                       refine=args.refine)
     if args.out:
         with open(args.out, "w") as f:
             json.dump({arch: table}, f, indent=1)
