@@ -1,24 +1,61 @@
 // W8A8 scaled matmul for MI355X (gfx950): the C entry points, the schedule dispatch and the
 // library's default configuration.  The schedules live in i8l_gemm_decode.hip (decode,
 // weights streamed or copied through LDS) and i8l_gemm_prefill.hip (macro tiles); the
-// generic kernel below takes any strides and alignment (correct, slow) and runs only when
-// the operands do not meet the fast schedules' layout requirements.
+// generic kernel below takes any strides and alignment and runs only when the operands do
+// not meet the fast schedules' layout requirements (an N-contiguous weight, a transposed or
+// unaligned activation, strides past 32 bits).
 #include "i8l_gemm.h"
 
 namespace i8l {
 
 // ------------------------------------------------------------------ generic schedule
+// Any strides, any alignment, any M, N, K (K = 0 included).  A workgroup of 4 waves computes
+// a 64 x 64 output tile in 64-byte K steps: the A and B tiles are gathered byte by byte into
+// LDS as [row][k] and [column][k] (zeros past M, N, K), with the lanes walking whichever index
+// of each operand has unit stride so the global reads coalesce, then each wave multiplies
+// its 16 token rows by the 4 column blocks with v_mfma_i32_16x16x64_i8, the fragment layout
+// of the decode schedules.  Outputs go through the scalar epilogue (any output stride).
 __global__ void __launch_bounds__(256)
 gemm_generic(const int8_t* __restrict__ A, int64_t sam, int64_t sak, const int8_t* __restrict__ B,
              int64_t sbk, int64_t sbn, Epi e, int64_t K) {
-  const int64_t n = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
-  const int64_t m = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (m >= e.M || n >= e.N) return;
-  int32_t acc = 0;
-  const int8_t* a = A + m * sam;
-  const int8_t* b = B + n * sbn;
-  for (int64_t k = 0; k < K; ++k) acc += (int32_t)a[k * sak] * (int32_t)b[k * sbk];
-  store1(e, m, n, acc);
+  __shared__ __attribute__((aligned(16))) int8_t As[64 * 64];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[64 * 64];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t ntn = (e.N + 63) / 64;  // column tiles; the grid is tiles of N x tiles of M
+  const int64_t m0 = (int64_t)(blockIdx.x / ntn) * 64, n0 = (int64_t)(blockIdx.x % ntn) * 64;
+  const bool a_k = sak == 1, b_k = sbk == 1 || sbn != 1;
+  v4i acc[4] = {};
+  for (int64_t k0 = 0; k0 < K; k0 += 64) {
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const int idx = i * 256 + t;  // 0..4095: (row, k) of the 64 x 64 tile
+      const int hi = idx >> 6, lo = idx & 63;
+      const int ra = a_k ? hi : lo, ka = a_k ? lo : hi;
+      const int64_t m = m0 + ra, ka_g = k0 + ka;
+      As[ra * 64 + ka] = (m < e.M && ka_g < K) ? A[m * sam + ka_g * sak] : (int8_t)0;
+      const int cb = b_k ? hi : lo, kb = b_k ? lo : hi;
+      const int64_t n = n0 + cb, kb_g = k0 + kb;
+      Bs[cb * 64 + kb] = (n < e.N && kb_g < K) ? B[kb_g * sbk + n * sbn] : (int8_t)0;
+    }
+    __syncthreads();
+    const v4i a = *(const v4i*)(As + (16 * wave + r16) * 64 + 16 * grp);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const v4i b = *(const v4i*)(Bs + (16 * f + r16) * 64 + 16 * grp);
+      acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, acc[f], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  const int64_t m = m0 + 16 * wave + r16;
+  if (m >= e.M) return;
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + 16 * f + 4 * grp + r;
+      if (n < e.N) store1(e, m, n, acc[f][r]);
+    }
 }
 
 void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
@@ -253,7 +290,13 @@ int w8a8_mm(const int8_t* a, int64_t stride_am, int64_t stride_ak, const int8_t*
   }
   hipError_t err;
   if (!fast || (wlds && !small_strides)) {
-    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 3) / 4));
+    const int64_t tiles = ((N + 63) / 64) * ((M + 63) / 64);
+    if (tiles > INT32_MAX) {
+      set_error("%s: %lld x %lld is too large for the generic kernel", who, (long long)M,
+                (long long)N);
+      return I8L_UNSUPPORTED;
+    }
+    const dim3 grid((unsigned)tiles);
     hipLaunchKernelGGL(gemm_generic, grid, dim3(256), 0, hs, a, stride_am, stride_ak, b,
                        stride_bk, stride_bn, e, K);
     err = hipGetLastError();

@@ -7,7 +7,14 @@
 //   fl_mfma    back-to-back v_mfma_i32_32x32x32_i8 (or v_mfma_i32_16x16x64_i8) on register
 //              operands, four independent accumulators a wave: the int8 MFMA rate the chip
 //              sustains under load, clock throttling included, on constant operands and on
-//              random ones (a GEMM's data toggles the multipliers, which costs power).
+//              random ones (a GEMM's data toggles the multipliers, which costs power);
+//   fl_place   a read of `bytes` that leaves each `granule`-byte chunk c in the L2 of XCD c % 8
+//              (workgroups are dealt to the 8 XCDs round-robin), the way a decode GEMM's
+//              workgroups later read them: how much a kernel gains when its weights were
+//              brought into its XCDs' caches by the launch before it;
+//   fl_ingest  each workgroup reading a 64 KiB window of an L2-resident buffer over and over,
+//              into registers or straight into LDS (global_load_lds_dwordx4): the rate at
+//              which a CU takes in operand bytes from L2 by either path.
 //
 // Every kernel's grid covers exactly its work (the read kernel's grid is the buffer's blocks,
 // whose size divides it, so every load is in bounds), and results reach memory only through a
@@ -86,6 +93,64 @@ __global__ __launch_bounds__(256) void fl_mfma_kernel(int iters, const v4i* __re
   }
 }
 
+// Workgroup b reads 4 KiB (16 bytes a thread) of the chunks that belong to XCD b % 8: its
+// (b / 8)-th 4 KiB piece of them, chunk c = b % 8 + 8 * (piece / pieces_per_chunk).
+__global__ __launch_bounds__(kReadThreads) void fl_place_kernel(const uint4* __restrict__ src,
+                                                                int64_t granule,
+                                                                uint32_t* __restrict__ out) {
+  const int64_t ppc = granule / 4096;  // 4 KiB pieces a chunk
+  const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int64_t chunk = x + 8 * (j / ppc);
+  const uint4* p = src + (chunk * granule + (j % ppc) * 4096) / 16 + threadIdx.x;
+  const uint4 v = *p;
+  const uint32_t h = v.x ^ v.y ^ v.z ^ v.w;
+  if (h == kNeverSeen) out[0] = h;
+}
+
+typedef __attribute__((address_space(3))) uint4 lds_u4;
+
+// Workgroup b reads window (b + 8 * it) % windows (64 KiB = 4096 uint4) at iteration it of
+// `iters` (the same XCD's windows when `windows` is a multiple of 8, so the buffer stays in
+// that XCD's L2, and a different address each iteration, so no load is loop-invariant); each
+// load instruction of a wave covers 1 KiB (16 bytes a lane), the wave's instructions
+// i * W + wave.
+// DIRECT: into a 64 KiB LDS buffer, all of a window's loads issued before one wait; else into
+// registers, folded by XOR after all of a window's loads are issued.
+template <bool DIRECT, int W>
+__global__ __launch_bounds__(64 * W) void fl_ingest_kernel(const uint4* __restrict__ src,
+                                                           int windows, int iters,
+                                                           uint32_t* __restrict__ out) {
+  extern __shared__ uint4 lds[];
+  constexpr int PER_WAVE = 4096 / (64 * W);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint32_t x = 0;
+  for (int it = 0; it < iters; ++it) {
+    const uint4* win = src + (int64_t)((blockIdx.x + 8 * it) % windows) * 4096;
+    if constexpr (DIRECT) {
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i) {
+        const int chunk = (i * W + wave) * 64;
+        __builtin_amdgcn_global_load_lds((const void*)(win + chunk + lane),
+                                         (lds_u4*)(lds + chunk), 16, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("" ::: "memory");
+    } else {
+      uint4 v[PER_WAVE];
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i) v[i] = win[(i * W + wave) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
+  }
+  if constexpr (DIRECT) {
+    __syncthreads();
+    x = lds[threadIdx.x].x;
+  }
+  if (x == kNeverSeen) out[0] = x;
+}
+
 int status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
 }  // namespace
@@ -137,6 +202,47 @@ int fl_mfma(int kind, int blocks, int iters, const void* data, int* out, void* s
     hipLaunchKernelGGL((fl_mfma_kernel<16, false>), grid, block, 0, st, iters, d, out);
   else
     return -1;
+  return status(hipGetLastError());
+}
+
+// Read `bytes` at the 16-byte aligned `src`, chunk c of `granule` bytes by XCD c % 8;
+// `granule` a multiple of 4 KiB and `bytes` a multiple of 8 * granule.
+int fl_place(const void* src, int64_t bytes, int64_t granule, uint32_t* out, void* stream) {
+  if (bytes <= 0 || granule <= 0 || granule % 4096 || bytes % (8 * granule) ||
+      ((uintptr_t)src & 15))
+    return -1;
+  const int64_t blocks = bytes / 4096;
+  if (blocks > 0x7fffffff) return -1;
+  hipLaunchKernelGGL(fl_place_kernel, dim3((unsigned)blocks), dim3(kReadThreads), 0,
+                     (hipStream_t)stream, (const uint4*)src, granule, out);
+  return status(hipGetLastError());
+}
+
+// `blocks` workgroups of `waves` (4 or 8) waves, each reading a 64 KiB window of `src`
+// (`windows` of them, 16-byte aligned) `iters` times, into LDS when `direct`, else into
+// registers; `out` is one uint32.
+int fl_ingest(const void* src, int windows, int blocks, int waves, int direct, int iters,
+              uint32_t* out, void* stream) {
+  if (windows < 1 || blocks < 1 || iters < 1 || ((uintptr_t)src & 15)) return -1;
+  const hipStream_t st = (hipStream_t)stream;
+  const uint4* s = (const uint4*)src;
+  const size_t shm = direct ? 64 << 10 : 0;
+  const dim3 grid(blocks);
+  if (direct && waves == 4) {
+    hipFuncSetAttribute((const void*)fl_ingest_kernel<true, 4>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    hipLaunchKernelGGL((fl_ingest_kernel<true, 4>), grid, dim3(256), shm, st, s, windows, iters, out);
+  } else if (direct && waves == 8) {
+    hipFuncSetAttribute((const void*)fl_ingest_kernel<true, 8>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    hipLaunchKernelGGL((fl_ingest_kernel<true, 8>), grid, dim3(512), shm, st, s, windows, iters, out);
+  } else if (!direct && waves == 4) {
+    hipLaunchKernelGGL((fl_ingest_kernel<false, 4>), grid, dim3(256), 0, st, s, windows, iters, out);
+  } else if (!direct && waves == 8) {
+    hipLaunchKernelGGL((fl_ingest_kernel<false, 8>), grid, dim3(512), 0, st, s, windows, iters, out);
+  } else {
+    return -1;
+  }
   return status(hipGetLastError());
 }
 

@@ -341,6 +341,67 @@ def test_exact_on_an_n_contiguous_weight():
     assert np.array_equal(np_(got), oracle_out(a, w, sa, sb, None, torch.float32))
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 64, 16), (3, 128, 48), (65, 256, 80), (130, 2048, 256),
+                                   (33, 512, 96), (200, 1024, 272), (7, 0, 16)])
+@pytest.mark.parametrize("layout", ["a_t_b_n", "a_k_b_n", "a_t_b_k", "a_strided_b_strided"])
+def test_generic_schedule_any_layout(m, k, n, layout):
+    """The generic kernel (any strides; M, N and K that are not multiples of its 64 x 64 x 64
+    tile, K = 0): transposed A (column-major), N-contiguous B, and both read through strided
+    views, against the oracle, int32 and bf16 with a bias and scalar scales.  The shapes pass
+    the reference's decline rule (N % bn, K % bk) under the default config."""
+    say(f"w8a8_mm generic m={m} k={k} n={n} {layout}")
+    a0, w0 = ints((m, k), 41 + m), ints((n, k), 42 + n)
+    if layout.startswith("a_t"):
+        a = a0.t().contiguous().t()                     # strides (1, M)
+    elif layout.startswith("a_strided"):
+        a = torch.zeros((m, 2 * k), dtype=torch.int8, device="cuda")[:, ::2]
+        a.copy_(a0)
+    else:
+        a = a0
+    if layout.endswith("b_n"):
+        b = w0.t().contiguous()                         # [K, N] row-major: strides (N, 1)
+    elif layout.endswith("b_strided"):
+        b = torch.zeros((k, 3 * n), dtype=torch.int8, device="cuda")[:, ::3]
+        b.copy_(w0.t())
+    else:
+        b = w0.t()                                      # K-contiguous (N, K) view
+    one = torch.ones(1, device="cuda")
+    acc = o.gemm_i32(np_(a0), np_(w0)) if k else np.zeros((m, n), np.int32)
+    assert np.array_equal(np_(w8a8_mm(a, b, one, one, raw=True)), acc)
+    g = torch.Generator().manual_seed(m * n + k)
+    sa = (torch.rand((1,), generator=g) * 1e-2 + 1e-3).cuda()
+    sb = (torch.rand((1,), generator=g) * 1e-2 + 1e-3).cuda()
+    bias = torch.randn(n, generator=g).to(torch.bfloat16).cuda()
+    out = w8a8_mm(a, b, sa, sb, torch.bfloat16, bias)
+    ref = o.epilogue(acc, np_(sa), np_(sb), bits(bias), o.BF16, o.BF16)
+    assert np.array_equal(bits(out), ref)
+
+
+def test_generic_schedule_is_not_a_scalar_loop():
+    """An N-contiguous weight at a decode shape takes the generic kernel; it must stay
+    within a small factor of the fast schedule on the same product (the scalar per-output
+    loop it replaced was ~100x slower)."""
+    m, k, n = 64, 2048, 2048
+    a, w = ints((m, k), 51), ints((n, k), 52)
+    b_n = w.t().contiguous()
+    one = torch.ones(1, device="cuda")
+    assert torch.equal(w8a8_mm(a, b_n, one, one, raw=True), w8a8_mm(a, w.t(), one, one, raw=True))
+
+    def timed(b):
+        for _ in range(3):
+            w8a8_mm(a, b, one, one, raw=True)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(20):
+            w8a8_mm(a, b, one, one, raw=True)
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / 20
+    fast, generic = timed(w.t()), timed(b_n)
+    say(f"generic {generic * 1e3:.1f} us vs fast {fast * 1e3:.1f} us")
+    assert generic < 20 * fast + 0.05
+
+
 def test_empty_batch():
     a = torch.empty((0, 2048), dtype=torch.int8, device="cuda")
     w = ints((1024, 2048), 1)
