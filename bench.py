@@ -758,7 +758,9 @@ def bench_floors(dev) -> dict:
         gate_up, of Llama-3-8B gate_up) rotating through >= 768 MiB of buffers so every read
         comes from HBM, and 8 MiB hot; the best of 1, 2, 4 and 8 loads a thread;
       * back-to-back int8 MFMAs on every SIMD: the rate sustained under load, on constant
-        operands and on random ones (toggling data costs power, and the clock follows)."""
+        operands and on random ones (toggling data costs power, and the clock follows);
+      * the rate at which CUs take in L2-resident bytes (each workgroup re-reading 64 KiB
+        windows that stay in its XCD's L2), into registers and straight into LDS."""
     import ctypes
 
     import torch
@@ -771,6 +773,8 @@ def bench_floors(dev) -> dict:
                           ctypes.c_void_p]
     L.fl_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                           ctypes.c_void_p, ctypes.c_void_p]
+    L.fl_ingest.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                            ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
 
     def stream():
         return torch.cuda.current_stream(dev).cuda_stream
@@ -818,8 +822,25 @@ def bench_floors(dev) -> dict:
             mfma.append([name, operands, round(us, 1), round(tops, 1),
                          round(tops / INT8_PEAK_TOPS, 3)])
             log(f"floor {name} {operands} operands: {tops:.0f} TOP/s")
+    ingest = []
+    window = torch.randint(-128, 128, (2 << 20,), dtype=torch.int8,
+                           generator=torch.Generator().manual_seed(1)).to(dev)
+    cus = props.multi_processor_count
+    for direct in (0, 1):
+        for blocks in (cus, 2 * cus):
+            iters = 128
+            us = graph_time_us(lambda i: ok(L.fl_ingest(window.data_ptr(), 32, blocks, 8, direct,
+                                                        iters, sink.data_ptr(), stream())), 5)
+            total = blocks * iters * 65536
+            ingest.append(["lds" if direct else "registers", blocks, round(us, 1),
+                           round(total / (us * 1e-6) / 1e12, 2),
+                           round(total / (us * 1e-6) / 1e9 / cus, 1)])
+            log(f"floor L2 ingest into {'LDS' if direct else 'registers'}, {blocks} workgroups: "
+                f"{total / (us * 1e-6) / 1e9 / cus:.0f} GB/s per CU")
     torch.cuda.empty_cache()
     return {"empty_kernel": {"cols": ["blocks", "threads", "us"], "rows": empty},
+            "l2_ingest": {"cols": ["into", "workgroups", "us", "TBps", "GBps_per_CU"],
+                          "rows": ingest, "waves_per_workgroup": 8, "window_KiB": 64},
             "read": {"cols": ["MiB", "cache", "us", "GBps", "hbm_frac", "loads_per_thread",
                               "us_by_loads_per_thread"], "rows": reads},
             "mfma": {"cols": ["instruction", "operands", "us", "TOPs", "frac_of_5000"],
