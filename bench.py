@@ -226,10 +226,12 @@ def schedule_of(cfg, k: int) -> str:
         return "gemm_stream"
     if cfg.stages == 2:
         return "gemm_staged"
-    if cfg.stages == 3 and cfg.bn <= 32:
+    if cfg.stages == 3 and cfg.bn <= 64:
         return "gemm_wlds1" if k == cfg.bk * cfg.warps else "gemm_wlds"
     if cfg.stages == 4 and cfg.bn <= 32:
         return "gemm_wlds1p"
+    if cfg.stages == 5 and cfg.bn <= 64:
+        return "gemm_wlds + splitk_sum"
     return "gemm_dmap" if cfg.stages >= 10 else "gemm_dma"
 
 
@@ -519,16 +521,18 @@ def bench_standin(dev) -> dict:
                     "> silu_mul_quant > down, one HIP graph per 28-layer step"}
 
 
-LLAMA_DECODE_M = [1, 4, 16]
+LLAMA_DECODE_M = [1, 4, 16, 64, 128]
 
 
 def bench_llama_decode(dev) -> dict:
     """Decode on the Llama-3-8B shapes (the larger of the two models BASELINE names for the
-    HBM target at M <= 16): µs per linear and fraction of 8 TB/s, weights rotating through
-    >= 768 MiB of copies so every call reads them from HBM."""
+    HBM target at M <= 16, and at 64 and 128 tokens, where down_proj splits K across
+    workgroups): µs per linear, fraction of 8 TB/s and the configuration, weights rotating
+    through >= 768 MiB of copies so every call reads them from HBM."""
     import torch
 
     from int8_linear import w8a8_mm
+    from int8_linear.kernel import choose_config
     from int8_linear.operands import operands, seed_of
     from int8_linear.shapes import SHAPES
     rows = []
@@ -548,11 +552,12 @@ def bench_llama_decode(dev) -> dict:
             us = graph_time_us(lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s,
                                                  torch.bfloat16), 2 * copies, 3)
             frac = gemm_bytes(m, k, n, False) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS
-            rows.append([label, m, round(us, 2), round(frac, 3)])
-            log(f"llama decode {label} M={m}: {us:.2f} us, {frac:.1%} of HBM")
+            cfg = choose_config(m, n, k)
+            rows.append([label, m, round(us, 2), round(frac, 3), f"{schedule_of(cfg, k)} {cfg.name}"])
+            log(f"llama decode {label} M={m}: {us:.2f} us, {frac:.1%} of HBM ({cfg.name})")
         del ws, d
         torch.cuda.empty_cache()
-    return {"cols": ["shape", "M", "us", "hbm_frac"], "rows": rows}
+    return {"cols": ["shape", "M", "us", "hbm_frac", "kernel"], "rows": rows}
 
 
 LAUNCH_SHAPES = [("q_proj, o_proj", 2048, 2048), ("gate_up_proj", 2048, 12288)]

@@ -301,8 +301,11 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   }
 
   // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
-  v4i* red = (v4i*)(lds + (size_t)W * nbuf * SB);  // [W][FR][64]
+  // The reduction area aliases the weight ring: every wave's last fragment reads of the ring
+  // are done at the barrier (no DMA is outstanding after the last step's wait).
+  v4i* red = (v4i*)lds;  // [W][FR][64]
   if (W > 1) {
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < MT; ++q)
 #pragma unroll
@@ -816,11 +819,20 @@ constexpr WldsTile kWlds[] = {{1, 16, 2}, {1, 16, 4}, {1, 16, 6}, {1, 16, 8}, {1
                               {4, 32, 4}, {1, 64, 2}, {2, 64, 2}, {4, 64, 2}, {1, 64, 4},
                               {2, 64, 4}};
 
+// LDS of gemm_wlds: the weight ring, or the reduction area of the partial products, which
+// aliases it, whichever is larger.
 size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
   const int64_t steps = K / ((int64_t)c.bk * c.warps);
   const int nbuf = steps > 1 ? 2 : 1;
   const int nf = c.bn > 16 ? c.bn / 16 : 1;  // 16-column fragments a wave reduces
-  return (size_t)c.warps * nbuf * c.bn * c.bk + (size_t)c.warps * (c.bm / 16) * nf * 1024;
+  const size_t ring = (size_t)c.warps * nbuf * c.bn * c.bk;
+  const size_t red = (size_t)c.warps * (c.bm / 16) * nf * 1024;
+  return std::max(ring, red);
+}
+
+// LDS of gemm_wlds1 (one step a wave): its weight buffers and, after them, the reduction area.
+size_t wlds1_lds_bytes(int mt, int nc, int ks, int W) {
+  return (size_t)W * nc * 64 * ks + (size_t)W * mt * (nc > 16 ? nc / 16 : 1) * 1024;
 }
 
 bool wlds1_built(int mt, int nc, int W, int ks);
@@ -836,7 +848,8 @@ bool wlds_ok(const i8l_config& c, int64_t K) {
   const bool one_step = K == (int64_t)c.bk * c.warps &&
                         wlds1_built(c.bm / 16, c.bn, c.warps, c.bk / 64);
   if (!one_step && !wlds_multi_fits(c.bm / 16, c.bn, c.bk / 64)) return false;
-  return wlds_lds_bytes(c, K) <= kMaxLds;
+  return (one_step ? wlds1_lds_bytes(c.bm / 16, c.bn, c.bk / 64, c.warps)
+                   : wlds_lds_bytes(c, K)) <= kMaxLds;
 }
 
 template <int MT, int NT, int NC>
@@ -872,7 +885,7 @@ template <int MT, int NC, int KS, int W, int EK>
 hipError_t launch_wlds1_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, hipStream_t st) {
   auto kern = gemm_wlds1<MT, NC, KS, W, EK>;
-  const size_t shm = (size_t)W * NC * 64 * KS + (size_t)W * MT * (NC > 16 ? NC / 16 : 1) * 1024;
+  const size_t shm = wlds1_lds_bytes(MT, NC, KS, W);
   static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
   lds_opt_in((const void*)kern, shm, lds_done);
   const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
@@ -952,14 +965,30 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
 // 64x64 tile moves half of what 32x32 tiles do; the split restores the workgroup count the
 // wide tile gives up.
 
-// One thread per 4 consecutive output columns of one row.
-template <int Z, int EK>
+// One thread per 4 consecutive output columns of one row.  XCD: pass 1 dealt each XCD the
+// contiguous columns [x, x+1) * N/8 (xcd_col_tile with N/bn a multiple of 8), so its partial
+// planes for those columns sit in that XCD's L2; workgroup b, which the dispatcher gives to
+// XCD b % 8, sums columns of that XCD's range and reads them there.  Correct either way.
+template <int Z, int EK, bool XCD>
 __global__ void __launch_bounds__(256)
 splitk_sum(const int32_t* __restrict__ ws, Epi e) {
-  const int nq = e.N >> 2;
-  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q >= (int64_t)e.M * nq) return;
-  const int64_t m = q / nq, n = (q - m * nq) * 4;
+  int64_t m, n;
+  if constexpr (XCD) {
+    const int qpr = e.N >> 5;  // quads a row within one XCD's columns
+    const int64_t u = (int64_t)(blockIdx.x >> 3) * 256 + threadIdx.x;
+    if (u >= (int64_t)e.M * qpr) return;
+    m = u / qpr;
+    n = (int64_t)(blockIdx.x & 7) * (e.N >> 3) + 4 * (u - m * qpr);
+  } else {
+    const int nq = e.N >> 2;
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= (int64_t)e.M * nq) return;
+    m = q / nq;
+    n = (q - m * nq) * 4;
+  }
+  // the epilogue operands and every partial are requested before any is used: one round trip
+  const Cols4 cl = load_cols4<EK>(e, n);
+  const float sam = load_sa<EK>(e, m);
   const int64_t plane = (int64_t)e.M * e.N;
   const int32_t* p = ws + m * e.N + n;
   v4i part[Z];
@@ -968,7 +997,7 @@ splitk_sum(const int32_t* __restrict__ ws, Epi e) {
   v4i sum = part[0];
 #pragma unroll
   for (int z = 1; z < Z; ++z) sum += part[z];
-  store4<EK>(e, m, n, sum);
+  store4s<EK>(e, m, n, sum, cl, sam);
 }
 
 int64_t wlds_split_workspace(const i8l_config& c, int64_t M, int64_t N) {
@@ -988,18 +1017,26 @@ bool wlds_split_ok(const i8l_config& c, int64_t K) {
   return wlds_lds_bytes(c, K / c.group_m) <= kMaxLds;
 }
 
-template <int Z>
-hipError_t launch_splitk_sum(const int32_t* ws, const Epi& e, hipStream_t st) {
+template <int Z, bool XCD>
+hipError_t launch_splitk_sum_x(const int32_t* ws, const Epi& e, hipStream_t st) {
   const int64_t quads = (int64_t)e.M * (e.N / 4);
-  const dim3 grid((unsigned)((quads + 255) / 256));
+  const dim3 grid((unsigned)(XCD ? 8 * ((quads / 8 + 255) / 256) : (quads + 255) / 256));
   switch (epi_kind(e)) {
-    case EK_BF16: hipLaunchKernelGGL((splitk_sum<Z, EK_BF16>), grid, dim3(256), 0, st, ws, e); break;
-    case EK_BF16_BBF16:
-      hipLaunchKernelGGL((splitk_sum<Z, EK_BF16_BBF16>), grid, dim3(256), 0, st, ws, e);
+    case EK_BF16:
+      hipLaunchKernelGGL((splitk_sum<Z, EK_BF16, XCD>), grid, dim3(256), 0, st, ws, e);
       break;
-    default: hipLaunchKernelGGL((splitk_sum<Z, EK_ANY>), grid, dim3(256), 0, st, ws, e);
+    case EK_BF16_BBF16:
+      hipLaunchKernelGGL((splitk_sum<Z, EK_BF16_BBF16, XCD>), grid, dim3(256), 0, st, ws, e);
+      break;
+    default: hipLaunchKernelGGL((splitk_sum<Z, EK_ANY, XCD>), grid, dim3(256), 0, st, ws, e);
   }
   return hipGetLastError();
+}
+
+template <int Z>
+hipError_t launch_splitk_sum(const int32_t* ws, const Epi& e, int nc, hipStream_t st) {
+  const bool xcd = (e.N / nc) % 8 == 0 && e.N % 32 == 0;
+  return xcd ? launch_splitk_sum_x<Z, true>(ws, e, st) : launch_splitk_sum_x<Z, false>(ws, e, st);
 }
 
 template <int MT, int NC, int KS>
@@ -1047,9 +1084,9 @@ hipError_t launch_wlds_split(const i8l_config& c, const int8_t* a, int64_t lda,
 #undef I8L_WLDS
   if (err != hipSuccess) return err;
   switch (c.group_m) {
-    case 2: return launch_splitk_sum<2>(ws, e, st);
-    case 4: return launch_splitk_sum<4>(ws, e, st);
-    case 8: return launch_splitk_sum<8>(ws, e, st);
+    case 2: return launch_splitk_sum<2>(ws, e, c.bn, st);
+    case 4: return launch_splitk_sum<4>(ws, e, c.bn, st);
+    case 8: return launch_splitk_sum<8>(ws, e, c.bn, st);
   }
   return hipErrorInvalidValue;
 }

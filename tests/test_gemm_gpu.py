@@ -584,13 +584,19 @@ SPLIT_TILES = [(1, 16, 2), (2, 32, 2), (4, 32, 2), (8, 16, 2), (1, 64, 2), (2, 6
 
 @pytest.mark.parametrize("tile", SPLIT_TILES, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
 @pytest.mark.parametrize("parts", [2, 4, 8])
-def test_split_of_k_is_exact(tile, parts):
+@pytest.mark.parametrize("waves,n", [(4, 512), (8, 512), (4, 192)])
+def test_split_of_k_is_exact(tile, parts, waves, n):
+    """n = 512 gives the sum kernel its XCD-local order (N / bn a multiple of 8), n = 192 the
+    plain one; 8 waves put the reduction area over the whole weight ring."""
     mt, nc, ks = tile
-    waves, n = 4, 512
+    if n % nc:
+        pytest.skip(f"N={n} is not whole {nc}-column tiles")
     for steps in (1, 2):
         k = 64 * ks * waves * steps * parts
         cfg = Config(16 * mt, nc, 64 * ks, waves, 5, parts)
-        assert kernel.supported(16 * mt, n, k, cfg), cfg.name
+        if not kernel.supported(16 * mt, n, k, cfg):
+            assert waves == 8, cfg.name       # every 4-wave split tile is built
+            pytest.skip(f"{cfg.name} is not built for K={k}")
         for m in sorted({1, 16 * mt - 3, 16 * mt}):
             say(f"w8a8_mm split m={m} k={k} n={n} config={cfg.name}")
             a, w = ints((m, k), 21 + m), ints((n, k), 22 + steps)
