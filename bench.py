@@ -765,7 +765,9 @@ def bench_floors(dev) -> dict:
       * back-to-back int8 MFMAs on every SIMD: the rate sustained under load, on constant
         operands and on random ones (toggling data costs power, and the clock follows);
       * the rate at which CUs take in L2-resident bytes (each workgroup re-reading 64 KiB
-        windows that stay in its XCD's L2), into registers and straight into LDS."""
+        windows that stay in its XCD's L2), into registers and straight into LDS;
+      * the LDS read rate of 16-byte-a-lane reads (the GEMMs' MFMA fragment reads) at 8 and
+        32 waves a CU."""
     import ctypes
 
     import torch
@@ -780,6 +782,8 @@ def bench_floors(dev) -> dict:
                           ctypes.c_void_p, ctypes.c_void_p]
     L.fl_ingest.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    L.fl_lds.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                         ctypes.c_void_p]
 
     def stream():
         return torch.cuda.current_stream(dev).cuda_stream
@@ -842,8 +846,19 @@ def bench_floors(dev) -> dict:
                            round(total / (us * 1e-6) / 1e9 / cus, 1)])
             log(f"floor L2 ingest into {'LDS' if direct else 'registers'}, {blocks} workgroups: "
                 f"{total / (us * 1e-6) / 1e9 / cus:.0f} GB/s per CU")
+    lds = []
+    for blocks in (cus, 4 * cus):
+        iters = 4096
+        us = graph_time_us(lambda i: ok(L.fl_lds(blocks, 512, iters, sink.data_ptr(),
+                                                 stream())), 3)
+        total = blocks * 512 * 16 * 8 * iters
+        lds.append([blocks * 8 // cus, round(us, 1), round(total / (us * 1e-6) / 1e9 / cus, 1)])
+        log(f"floor LDS reads, {blocks * 8 // cus} waves a CU: "
+            f"{total / (us * 1e-6) / 1e9 / cus:.0f} GB/s per CU")
     torch.cuda.empty_cache()
     return {"empty_kernel": {"cols": ["blocks", "threads", "us"], "rows": empty},
+            "lds_read": {"cols": ["waves_per_CU", "us", "GBps_per_CU"], "rows": lds,
+                         "read": "ds_read_b128, 8 in flight a wave, conflict-free"},
             "l2_ingest": {"cols": ["into", "workgroups", "us", "TBps", "GBps_per_CU"],
                           "rows": ingest, "waves_per_workgroup": 8, "window_KiB": 64},
             "read": {"cols": ["MiB", "cache", "us", "GBps", "hbm_frac", "loads_per_thread",

@@ -12,6 +12,9 @@
 //              (workgroups are dealt to the 8 XCDs round-robin), the way a decode GEMM's
 //              workgroups later read them: how much a kernel gains when its weights were
 //              brought into its XCDs' caches by the launch before it;
+//   fl_lds     waves reading 16 bytes a lane from LDS (ds_read_b128, the MFMA fragment read
+//              of the GEMMs, conflict-free addresses) as fast as they can: the CU's LDS read
+//              rate, the budget a GEMM's fragment reads and direct-to-LDS writes share;
 //   fl_ingest  each workgroup reading a 64 KiB window of an L2-resident buffer over and over,
 //              into registers or straight into LDS (global_load_lds_dwordx4): the rate at
 //              which a CU takes in operand bytes from L2 by either path.
@@ -105,6 +108,26 @@ __global__ __launch_bounds__(kReadThreads) void fl_place_kernel(const uint4* __r
   const uint4 v = *p;
   const uint32_t h = v.x ^ v.y ^ v.z ^ v.w;
   if (h == kNeverSeen) out[0] = h;
+}
+
+// Each wave reads 16 bytes a lane from a 64 KiB LDS buffer, U independent reads in flight,
+// `iters` rounds; lane l of read u at byte ((u * W + wave) * 64 + l) * 16 mod 64 KiB, so a
+// wave's read covers 1 KiB of consecutive bytes (no bank conflicts).
+template <int U>
+__global__ __launch_bounds__(512) void fl_lds_kernel(int iters, uint32_t* __restrict__ out) {
+  __shared__ uint4 buf[4096];
+  const int t = threadIdx.x, W = blockDim.x >> 6, wave = t >> 6, lane = t & 63;
+  for (int i = t; i < 4096; i += blockDim.x) buf[i] = make_uint4(i, i * 3, i * 5, i * 7);
+  __syncthreads();
+  uint32_t x = 0;
+  for (int it = 0; it < iters; ++it) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = buf[(((it * U + u) * W + wave) * 64 + lane) & 4095];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (x == kNeverSeen) out[0] = x;
 }
 
 typedef __attribute__((address_space(3))) uint4 lds_u4;
@@ -202,6 +225,15 @@ int fl_mfma(int kind, int blocks, int iters, const void* data, int* out, void* s
     hipLaunchKernelGGL((fl_mfma_kernel<16, false>), grid, block, 0, st, iters, d, out);
   else
     return -1;
+  return status(hipGetLastError());
+}
+
+// `blocks` workgroups of `threads` (64..512, a multiple of 64), each wave `iters` rounds of 8
+// independent 16-byte LDS reads a lane; `out` is one uint32.
+int fl_lds(int blocks, int threads, int iters, uint32_t* out, void* stream) {
+  if (blocks < 1 || iters < 1 || threads < 64 || threads > 512 || threads % 64) return -1;
+  hipLaunchKernelGGL(fl_lds_kernel<8>, dim3(blocks), dim3(threads), 0, (hipStream_t)stream,
+                     iters, out);
   return status(hipGetLastError());
 }
 
