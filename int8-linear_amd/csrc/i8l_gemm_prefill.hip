@@ -141,8 +141,10 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
     const int i = tid + j * T;
     const int r = i / CPR, c8 = i % CPR;
     const int64_t m = m0 + r;
-    const uint4 v = *(const uint4*)(lds + r * PITCH + 16 * c8);
-    if (m < e.M) *(uint4*)((uint16_t*)e.out + m * e.ldc + n0 + 8 * c8) = v;
+    const v4i v = *(const v4i*)(lds + r * PITCH + 16 * c8);
+    // the output is written once and read by the next operation, not by this one: stream it
+    // past the caches, which keep the operand panels the other tiles still read
+    if (m < e.M) __builtin_nontemporal_store(v, (v4i*)((uint16_t*)e.out + m * e.ldc + n0 + 8 * c8));
   }
 }
 
