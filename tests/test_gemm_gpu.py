@@ -677,3 +677,37 @@ def test_split_of_k_needs_a_workspace_and_replays_in_a_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert np.array_equal(bits(got), oracle_out(a, w, sa, sb, None, torch.bfloat16)), seed
+
+
+def test_random_configs_against_the_oracle():
+    """Seeded random cases over the whole built configuration space: a random shape, a
+    random configuration from the tuner's candidates for it (every schedule family: weight
+    streaming, weights through LDS, persistent, split of K, prefill tiles), random scale
+    layouts, bias and output dtype; each output against the oracle bit for bit."""
+    from int8_linear.tune import candidate_configs
+    rng = np.random.default_rng(2026)
+    ks = [1024, 2048, 3072, 4096, 6144]
+    ns = [256, 512, 768, 1024, 2048]
+    ms = [1, 2, 3, 7, 16, 17, 31, 48, 64, 100, 128, 200, 256, 300, 513]
+    cases = 0
+    families = set()
+    while cases < 120:
+        m, k, n = int(rng.choice(ms)), int(rng.choice(ks)), int(rng.choice(ns))
+        cands = candidate_configs(m, k, n)
+        if not cands:
+            continue
+        cfg = cands[int(rng.integers(len(cands)))]
+        families.add(cfg.stages if cfg.stages < 10 else 10)
+        say(f"random case {cases}: m={m} k={k} n={n} {cfg.name}")
+        a, w = ints((m, k), 1000 + cases), ints((n, k), 2000 + cases)
+        g = torch.Generator().manual_seed(cases)
+        per_row, per_col = bool(rng.integers(2)), bool(rng.integers(2))
+        sa = (torch.rand((m, 1) if per_row else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+        sb = (torch.rand((n, 1) if per_col else (1,), generator=g) * 1e-2 + 1e-3).cuda()
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        bias_dt = [None, torch.bfloat16, torch.float32][int(rng.integers(3))]
+        bias = torch.randn(n, generator=g).to(bias_dt).cuda() if bias_dt else None
+        out = w8a8_mm(a, w.t(), sa, sb, dtype, bias, config=cfg)
+        assert np.array_equal(as_np(out), oracle_out(a, w, sa, sb, bias, dtype)), (m, k, n, cfg)
+        cases += 1
+    assert families >= {1, 3, 4, 5, 10}, families
