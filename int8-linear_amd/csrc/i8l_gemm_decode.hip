@@ -180,7 +180,7 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
   constexpr int AL = MT * KS;                // activation loads per lane per step
   constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
-  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int NF = NC / NCF;               // column fragments of the tile (64 columns: 4)
   constexpr int FR = MT * NF;                // output fragments, numbered i * NF + f
   static_assert(NF * NCF == NC, "the tile must be whole column fragments");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
@@ -353,7 +353,7 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
   constexpr int NI = SB / 1024;
   static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
   constexpr int NCF = NC < 16 ? NC : 16;     // output columns of one MFMA fragment
-  constexpr int NF = NC / NCF;               // column fragments of the tile (32 columns: 2)
+  constexpr int NF = NC / NCF;               // column fragments of the tile (64 columns: 4)
   constexpr int FR = MT * NF;                // output fragments of the tile
   static_assert(NF * NCF == NC, "the tile must be whole column fragments");
   static_assert(FR <= W, "every fragment needs a storing wave");
