@@ -164,6 +164,53 @@ __device__ __forceinline__ void wait_vmcnt_wlds() {
 
 typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 
+// The end of the multi-step weights-through-LDS tiles: sum the W waves' partial products
+// (int32 addition is exact and order-free) through an LDS area that aliases the step ring
+// (every wave's last fragment reads of the ring are done at the first barrier, and no DMA
+// is outstanding after the last step's wait), then the epilogue; fragment fr = i * NF + f is
+// stored by wave fr % W, which loaded its epilogue operands (cl0, sa0) early when fr == wave.
+template <int MT, int NC, int EK>
+__device__ __forceinline__ void wlds_sum_store(const v4i (&acc)[MT][NC < 16 ? 1 : NC / 16],
+                                               int8_t* lds, const Epi& e, int W, int wave,
+                                               int lane, int64_t m0, int64_t n0,
+                                               const Cols4& cl0, float sa0) {
+  constexpr int NCF = NC < 16 ? NC : 16;
+  constexpr int NF = NC / NCF;
+  constexpr int FR = MT * NF;
+  const int r16 = lane & 15, grp = lane >> 4;
+  v4i* red = (v4i*)lds;  // [W][FR][64]
+  if (W > 1) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) red[(wave * FR + q * NF + f) * 64 + lane] = acc[q][f];
+    __syncthreads();
+  }
+  for (int fr = wave; fr < FR; fr += W) {
+    v4i sum;
+    if (W > 1) {
+      sum = red[fr * 64 + lane];
+      for (int w = 1; w < W; ++w) sum += red[(w * FR + fr) * 64 + lane];
+    } else {
+      sum = acc[0][0];
+#pragma unroll
+      for (int q = 0; q < MT; ++q)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          if (q * NF + f == fr) sum = acc[q][f];
+    }
+    const int64_t m = m0 + 16 * (fr / NF) + r16;
+    const int64_t n = n0 + NCF * (fr % NF) + 4 * grp;
+    if (m < e.M && 4 * grp < NCF) {
+      if (fr == wave)
+        store4s<EK>(e, m, n, sum, cl0, sa0);
+      else
+        store4<EK>(e, m, n, sum);
+    }
+  }
+}
+
 template <int MT, int NC, int KS, int EK>
 __global__ void __launch_bounds__(wlds_bound(MT, KS, NC))
 gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
@@ -300,40 +347,133 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     compute(a0, i);
   }
 
-  // Sum the W partial products (int32 addition is exact and order-free), then epilogue.
-  // The reduction area aliases the weight ring: every wave's last fragment reads of the ring
-  // are done at the barrier (no DMA is outstanding after the last step's wait).
-  v4i* red = (v4i*)lds;  // [W][FR][64]
-  if (W > 1) {
-    __syncthreads();
+  wlds_sum_store<MT, NC, EK>(acc, lds, e, W, wave, lane, m0, n0, cl0, sa0);
+}
+
+// gemm_wlds with the activations copied through LDS too: a wave's step buffer holds its NC
+// weight rows and then its 16*MT activation rows, S bytes each (same swizzle), all filled by
+// global_load_lds_dwordx4 in whole row segments, and both MFMA operands are read from LDS in
+// the fragment layout.  gemm_wlds loads the activations straight into the fragment layout
+// (16 rows x 64 bytes an instruction: half a cache line a row per request); from 32 tokens
+// on, where a CU takes in as many activation bytes as weight bytes, that costs 20-40% of
+// the kernel.  Rows past M read the tile's first row (always valid) and are never stored.
+template <int MT, int NC, int KS, int EK>
+__global__ void __launch_bounds__(wlds_bound(MT, KS, NC))
+gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
+            int64_t ldb, Epi e, int steps, int nbuf) {
+  constexpr int S = 64 * KS;
+  constexpr int CPR = S / 16;
+  constexpr int CPR_LOW = CPR & -CPR;
+  constexpr int SWM = (CPR_LOW < 16 ? CPR_LOW : 16) - 1;
+  static_assert(CPR % (SWM + 1) == 0, "the swizzle must permute the row's chunks");
+  constexpr int ROWS = NC + 16 * MT;         // weight rows, then activation rows
+  constexpr int SB = ROWS * S;               // bytes per wave per step
+  constexpr int NI = SB / 1024;              // DMA instructions per wave per step
+  static_assert(NI * 1024 == SB, "a step must be whole 1 KiB DMA instructions");
+  static_assert(NI < 64, "one step's DMA must fit the vmcnt counter");
+  constexpr int NCF = NC < 16 ? NC : 16;
+  constexpr int NF = NC / NCF;
+  constexpr int FR = MT * NF;
+  static_assert(NF * NCF == NC, "the tile must be whole column fragments");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int64_t n0 = xcd_col_tile() * NC;
+  const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
+  const int64_t kw = (int64_t)(blockIdx.z * W + wave) * steps * S;
+  if (gridDim.z > 1) e.out = (int32_t*)e.out + (int64_t)blockIdx.z * e.M * e.ldc;
+  int8_t* wbuf = lds + (size_t)wave * nbuf * SB;
+
+  // DMA sources: instruction t writes buffer bytes [t*1024, t*1024+1024), lane l the 16 bytes
+  // at +16*l: row o / S (weight row r < NC, else activation row r - NC), slot (o % S) / 16.
+  // In-tile row offsets (< 64 weight rows, < 128 token rows) fit 32 bits.
+  const int8_t* Bw = B + n0 * ldb + kw;
+  const int8_t* Aw = A + m0 * lda + kw;
+  const int ldb32 = (int)ldb, lda32 = (int)lda;
+  const int8_t* gsrc[NI];
 #pragma unroll
-    for (int q = 0; q < MT; ++q)
-#pragma unroll
-      for (int f = 0; f < NF; ++f) red[(wave * FR + q * NF + f) * 64 + lane] = acc[q][f];
-    __syncthreads();
+  for (int t = 0; t < NI; ++t) {
+    const int o = t * 1024 + 16 * lane;
+    const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+    const int ml = r - NC;
+    gsrc[t] = r < NC ? Bw + (r * ldb32 + 16 * c)
+                     : Aw + ((m0 + ml < e.M ? ml * lda32 : 0) + 16 * c);
   }
-  for (int fr = wave; fr < FR; fr += W) {
-    v4i sum;
-    if (W > 1) {
-      sum = red[fr * 64 + lane];
-      for (int w = 1; w < W; ++w) sum += red[(w * FR + fr) * 64 + lane];
-    } else {
-      sum = acc[0][0];
+  // fragment read offsets of one step: weight fragment f's row br, activation fragment i's
+  // row NC + 16 i + r16, chunk 4s + grp
+  int bofs[KS][NF], aofs[KS][MT];
 #pragma unroll
-      for (int q = 0; q < MT; ++q)
+  for (int s = 0; s < KS; ++s) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int br = NCF * f + r16 % NCF;
+      bofs[s][f] = br * S + 16 * ((4 * s + grp) ^ (br & SWM));
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int ar = NC + 16 * i + r16;
+      aofs[s][i] = ar * S + 16 * ((4 * s + grp) ^ (ar & SWM));
+    }
+  }
+
+  v4i acc[MT][NF];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[i][f] = v4i{0, 0, 0, 0};
+
+  // `fenced` as in gemm_wlds: the previous step's fragment reads stay above the issue
+  auto issue = [&](int step, bool fenced) {
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+    lds_i8_t* dst = (lds_i8_t*)(wbuf + (step % nbuf) * SB);
+    const int64_t ko = (int64_t)step * S;
+#pragma unroll
+    for (int t = 0; t < NI; ++t)
+      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
+    if (fenced) __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](int step) {
+    const int8_t* base = wbuf + (step % nbuf) * SB;
+    v4i b[KS][NF], a[KS][MT];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) b[s][f] = *(const v4i*)(base + bofs[s][f]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) a[s][i] = *(const v4i*)(base + aofs[s][i]);
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int f = 0; f < NF; ++f)
-          if (q * NF + f == fr) sum = acc[q][f];
-    }
-    const int64_t m = m0 + 16 * (fr / NF) + r16;
-    const int64_t n = n0 + NCF * (fr % NF) + 4 * grp;
-    if (m < e.M && 4 * grp < NCF) {
-      if (fr == wave)
-        store4s<EK>(e, m, n, sum, cl0, sa0);
-      else
-        store4<EK>(e, m, n, sum);
-    }
+          acc[i][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s][i], acc[i][f], 0, 0, 0);
+  };
+
+  issue(0, steps > 1);
+  Cols4 cl0;
+  float sa0 = 0.0f;
+  if (wave < FR && 4 * grp < NCF) {
+    const int64_t m = m0 + 16 * (wave / NF) + r16;
+    cl0 = load_cols4<EK>(e, n0 + NCF * (wave % NF) + 4 * grp);
+    sa0 = load_sa<EK>(e, m < e.M ? m : 0);
   }
+  // each step's copy is requested before the wait for the one before, which leaves exactly
+  // one step's DMA outstanding (the epilogue operands were requested between steps 0 and 1,
+  // so they have landed too)
+  int i = 0;
+  for (; i + 1 < steps; ++i) {
+    issue(i + 1, true);
+    wait_vmcnt_wlds<NI>();
+    compute(i);
+  }
+  wait_vmcnt_wlds<0>();
+  compute(i);
+  wlds_sum_store<MT, NC, EK>(acc, lds, e, W, wave, lane, m0, n0, cl0, sa0);
 }
 
 // The same tile when every wave's K slice is a single step (K == W * 64 * KS), with the
@@ -830,6 +970,17 @@ size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
   return std::max(ring, red);
 }
 
+// LDS of gemm_wlds_a: the step ring of weight and activation rows, or the reduction area
+// that aliases it, whichever is larger.
+size_t wlds_a_lds_bytes(const i8l_config& c, int64_t K) {
+  const int64_t steps = K / ((int64_t)c.bk * c.warps);
+  const int nbuf = steps > 1 ? 2 : 1;
+  const int nf = c.bn > 16 ? c.bn / 16 : 1;
+  const size_t ring = (size_t)c.warps * nbuf * (c.bn + c.bm) * c.bk;
+  const size_t red = (size_t)c.warps * (c.bm / 16) * nf * 1024;
+  return std::max(ring, red);
+}
+
 // LDS of gemm_wlds1 (one step a wave): its weight buffers and, after them, the reduction area.
 size_t wlds1_lds_bytes(int mt, int nc, int ks, int W) {
   return (size_t)W * nc * 64 * ks + (size_t)W * mt * (nc > 16 ? nc / 16 : 1) * 1024;
@@ -867,18 +1018,36 @@ hipError_t launch_stream_u(const int8_t* a, int64_t lda, const int8_t* b, int64_
   return hipGetLastError();
 }
 
+// The multi-step tile over `parts` equal parts of K (grid z; 1 = no split): with the
+// activations copied through LDS when both rings fit (gemm_wlds_a), else loaded into
+// registers (gemm_wlds).
+template <int MT, int NC, int KS, int EK>
+hipError_t launch_wlds_steps(const i8l_config& c, const int8_t* a, int64_t lda,
+                             const int8_t* b, int64_t ldb, const Epi& e, int64_t kpart,
+                             int parts, hipStream_t st) {
+  const int steps = (int)(kpart / ((int64_t)c.bk * c.warps));
+  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT), parts);
+  const size_t shm_a = wlds_a_lds_bytes(c, kpart);
+  if (shm_a <= kMaxLds) {
+    auto kern = gemm_wlds_a<MT, NC, KS, EK>;
+    static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+    lds_opt_in((const void*)kern, kMaxLds, lds_done);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm_a, st, a, lda, b, ldb, e, steps,
+                       steps > 1 ? 2 : 1);
+  } else {
+    auto kern = gemm_wlds<MT, NC, KS, EK>;
+    static std::atomic<uint64_t> lds_done{0};
+    lds_opt_in((const void*)kern, kMaxLds, lds_done);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), wlds_lds_bytes(c, kpart), st, a, lda, b,
+                       ldb, e, steps, steps > 1 ? 2 : 1);
+  }
+  return hipGetLastError();
+}
+
 template <int MT, int NC, int KS, int EK>
 hipError_t launch_wlds_k(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
-  auto kern = gemm_wlds<MT, NC, KS, EK>;
-  const size_t shm = wlds_lds_bytes(c, K);
-  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
-  lds_opt_in((const void*)kern, kMaxLds, lds_done);
-  const int steps = (int)(K / ((int64_t)c.bk * c.warps));
-  const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT));
-  hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
-                     steps > 1 ? 2 : 1);
-  return hipGetLastError();
+  return launch_wlds_steps<MT, NC, KS, EK>(c, a, lda, b, ldb, e, K, 1, st);
 }
 
 template <int MT, int NC, int KS, int W, int EK>
@@ -1042,18 +1211,9 @@ hipError_t launch_splitk_sum(const int32_t* ws, const Epi& e, int nc, hipStream_
 template <int MT, int NC, int KS>
 hipError_t launch_wlds_part(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                             int64_t ldb, const Epi& e, int64_t K, hipStream_t st) {
-  if constexpr (wlds_multi_fits(MT, NC, KS)) {
-    auto kern = gemm_wlds<MT, NC, KS, EK_ANY>;
-    const int64_t kpart = K / c.group_m;
-    const size_t shm = wlds_lds_bytes(c, kpart);
-    static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
-    lds_opt_in((const void*)kern, kMaxLds, lds_done);
-    const int steps = (int)(kpart / ((int64_t)c.bk * c.warps));
-    const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT), c.group_m);
-    hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm, st, a, lda, b, ldb, e, steps,
-                       steps > 1 ? 2 : 1);
-    return hipGetLastError();
-  }
+  if constexpr (wlds_multi_fits(MT, NC, KS))
+    return launch_wlds_steps<MT, NC, KS, EK_ANY>(c, a, lda, b, ldb, e, K / c.group_m,
+                                                 c.group_m, st);
   return hipErrorInvalidValue;
 }
 
