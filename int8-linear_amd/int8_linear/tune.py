@@ -183,15 +183,14 @@ def time_cold_us(call, copies: int, windows: int = 3) -> float:
 
 
 def refine_candidates(m: int, k: int, n: int) -> list[Config]:
-    """The configuration tuned_config holds now (else the default) and the schedule families
-    added after the table was made: 64-column weights-through-LDS tiles, the split of K
-    (stages 5) and the multi-step tiles of 8 or more waves that fit once the reduction area
-    shared the weight ring.  Timing only these against the entry they would replace updates
-    a table without re-timing every candidate of every bucket."""
+    """The configuration tuned_config holds now (else the default) and the schedules that
+    changed after the table was made: every weights-through-LDS tile (stages 3: 64-column
+    tiles, 8 or more waves now that the reduction area shares the ring, activations copied
+    through LDS) and the split of K (stages 5).  Timing only these against the entry they
+    would replace updates a table without re-timing every candidate of every bucket."""
     from int8_linear.kernel import tuned_config
     cur = tuned_config(m, n, k) or default_config(m, n, k)
-    new = [c for c in candidate_configs(m, k, n)
-           if c.stages == 5 or (c.stages == 3 and (c.bn == 64 or c.warps >= 8))]
+    new = [c for c in candidate_configs(m, k, n) if c.stages in (3, 5)]
     return [cur] + [c for c in new if c != cur]
 
 
