@@ -261,6 +261,42 @@ def test_weights_through_lds_schedule(tile, steps, waves):
         assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.float16))
 
 
+def _wlds_a_lds(mt, nc, ks, w):
+    """LDS bytes of the activations-through-LDS multi-step tile (two step buffers of weight
+    and activation rows a wave, or the cross-wave reduction area, the larger)."""
+    ring = w * 2 * (16 * mt + nc) * 64 * ks
+    red = w * mt * (nc // 16 if nc > 16 else 1) * 1024
+    return max(ring, red)
+
+
+# (mt, nc, ks, waves): the first two copy the activations through LDS with the weights, the
+# last two need more LDS than a CU has for that and load them into registers instead
+MULTI_STEP = [(2, 32, 4, 4), (1, 16, 4, 4), (4, 64, 2, 8), (2, 32, 4, 8)]
+
+
+@pytest.mark.parametrize("tile", MULTI_STEP, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}_w{t[3]}")
+def test_multi_step_tiles_every_epilogue(tile):
+    """Both multi-step decode kernels (gemm_wlds_a, and gemm_wlds where its rings do not fit)
+    through every output dtype, bias dtype and scale layout, bit-exact against the oracle."""
+    mt, nc, ks, w_ = tile
+    assert (_wlds_a_lds(*tile) <= 160 * 1024) == (tile in MULTI_STEP[:2])
+    m, k, n = 16 * mt - 3, 64 * ks * w_ * 3, 512
+    cfg = Config(16 * mt, nc, 64 * ks, w_, 3, 1)
+    assert kernel.supported(m, n, k, cfg), cfg.name
+    a, w = ints((m, k), 41 + mt), ints((n, k), 42 + nc)
+    g = torch.Generator().manual_seed(43)
+    sa_row = (torch.rand((m, 1), generator=g) * 1e-2 + 1e-3).cuda()
+    sb_col = (torch.rand((n, 1), generator=g) * 1e-2 + 1e-3).cuda()
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        for bias_dtype in (None, torch.bfloat16, torch.float16, torch.float32):
+            say(f"multi-step {cfg.name} m={m} k={k} {dtype} bias={bias_dtype}")
+            bias = torch.randn(n, generator=g).to(bias_dtype).cuda() if bias_dtype else None
+            for sa, sb in ((sa_row, sb_col), (sa_row[:1].reshape(1), sb_col[:1].reshape(1))):
+                out = w8a8_mm(a, w.t(), sa, sb, dtype, bias, config=cfg)
+                assert np.array_equal(as_np(out), oracle_out(a, w, sa, sb, bias, dtype)), \
+                    (dtype, bias_dtype, sa.numel(), sb.numel())
+
+
 @pytest.mark.parametrize("m", [37, 13])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("per_row", [True, False])
