@@ -57,7 +57,9 @@ __device__ __forceinline__ void load_tile_cols_k(const Epi& e, int64_t nb, Cols4
         for (int r = 0; r < 4; ++r)
           c.bias[r] = BD == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
       } else {
-        c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = 0.0f;
+        // no bias: -0, the identity of IEEE addition (x + -0 == x for every x, -0 and NaN
+        // included), so the epilogue adds the bias without a test
+        c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = -0.0f;
       }
     }
 }
@@ -103,34 +105,41 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
     const int64_t m = m0 + wm * TM + b * 32 + frow;
     sam[b] = load_sa(e, m < e.M ? m : 0);
   }
-  const bool bf = e.out_dtype == I8L_BF16;
   Cols4 cls[FA][4];
   if (e.sb_per_col)
     load_tile_cols_s<FA, true>(e, n0 + wn * TN + 4 * fhalf, cls);
   else
     load_tile_cols_s<FA, false>(e, n0 + wn * TN + 4 * fhalf, cls);
+  // the output dtype is uniform: one copy of the conversion loop per dtype, no per-value select
+  auto stage = [&](auto pack2) {
 #pragma unroll
-  for (int a = 0; a < FA; ++a) {
-    const Cols4 (&cl)[4] = cls[a];
+    for (int a = 0; a < FA; ++a) {
+      const Cols4 (&cl)[4] = cls[a];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = wn * TN + a * 32 + 8 * q + 4 * fhalf;  // column within the tile
+      for (int q = 0; q < 4; ++q) {
+        const int c = wn * TN + a * 32 + 8 * q + 4 * fhalf;  // column within the tile
 #pragma unroll
-      for (int b = 0; b < FB; ++b) {
-        const int r = wm * TM + b * 32 + frow;             // row within the tile
-        uint32_t h[4];
+        for (int b = 0; b < FB; ++b) {
+          const int r = wm * TM + b * 32 + frow;             // row within the tile
+          float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = (float)acc[a][b][4 * q + i];
-          v = v * sam[b];
-          v = v * cl[q].sb[i];
-          if (e.bias_dtype != I8L_DTYPE_NONE) v = v + cl[q].bias[i];
-          h[i] = bf ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+          for (int i = 0; i < 4; ++i) {
+            v[i] = (float)acc[a][b][4 * q + i];
+            v[i] = v[i] * sam[b];
+            v[i] = v[i] * cl[q].sb[i];
+            v[i] = v[i] + cl[q].bias[i];
+          }
+          *(uint2*)(lds + r * PITCH + 2 * c) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
         }
-        *(uint2*)(lds + r * PITCH + 2 * c) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
       }
     }
-  }
+  };
+  if (e.out_dtype == I8L_BF16)
+    stage([](float x, float y) { return f32x2_to_bf16x2_bits(x, y); });
+  else
+    stage([](float x, float y) {
+      return (uint32_t)f32_to_f16_bits(x) | ((uint32_t)f32_to_f16_bits(y) << 16);
+    });
   // Other waves read these stores: the barrier must also wait for them to complete
   // (s_barrier alone does not, and with two workgroups a CU sharing the LDS they do lag).
   __syncthreads();
