@@ -190,7 +190,8 @@ def refine_candidates(m: int, k: int, n: int) -> list[Config]:
     would replace updates a table without re-timing every candidate of every bucket."""
     from int8_linear.kernel import tuned_config
     cur = tuned_config(m, n, k) or default_config(m, n, k)
-    new = [c for c in candidate_configs(m, k, n) if c.stages in (3, 5)]
+    # stages 3 and 5 with bn <= 64; wider tiles at those stages are prefill rings (gemm_dma)
+    new = [c for c in candidate_configs(m, k, n) if c.stages in (3, 5) and c.bn <= 64]
     return [cur] + [c for c in new if c != cur]
 
 
@@ -258,8 +259,8 @@ def main() -> int:
                     help="comma-separated KxN shapes of the preset to tune (default: all)")
     ap.add_argument("--merge", action="store_true", help="write the result into tuned_configs.json")
     ap.add_argument("--refine", action="store_true",
-                    help="time only the current table entry against the newer schedule "
-                         "families (64-column tiles, split of K)")
+                    help="time only the current table entry against the weights-through-LDS "
+                         "tiles and the split of K (stages 3 and 5)")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
     dev = torch.device("cuda:0")

@@ -279,3 +279,59 @@ def test_situ_tune_writes_only_kept_sets_as_table_rows():
     for r in rows.values():
         assert r == {"8": {"config": cfg, "stand_in_us": 30.9}}
     assert 0 < situ_tune.ACCEPT < 0.05
+
+
+def test_tuner_merge_updates_rows_and_keeps_the_rest(tmp_path):
+    """tune.merge writes {"KxN": {M: row}} under the device key, replacing the buckets it is
+    given and keeping every other bucket, shape and device (reference merge:
+    bench/bench_linear.py:385-389)."""
+    import json
+
+    from int8_linear import tune
+    path = tmp_path / "table.json"
+    row = lambda us: {"config": {"bm": 16, "bn": 16, "bk": 256, "warps": 4, "stages": 3,
+                                 "group_m": 1}, "graph_us": us, "default_us": us}
+    path.write_text(json.dumps({"gfx950": {"2048x4096": {"1": row(4.0), "16": row(5.0)},
+                                           "6144x2048": {"1": row(6.0)}},
+                                "other": {"2048x4096": {"1": row(9.0)}}}))
+    tune.merge({"2048x4096": {"16": row(4.5), "32": row(5.5)}, "4096x4096": {"1": row(7.0)}},
+               "gfx950", path=path)
+    t = json.loads(path.read_text())
+    assert path.read_text().endswith("\n")
+    dev = t["gfx950"]
+    assert dev["2048x4096"]["1"]["graph_us"] == 4.0          # untouched bucket
+    assert dev["2048x4096"]["16"]["graph_us"] == 4.5         # replaced
+    assert dev["2048x4096"]["32"]["graph_us"] == 5.5         # added
+    assert dev["6144x2048"] == {"1": row(6.0)} and dev["4096x4096"] == {"1": row(7.0)}
+    assert t["other"] == {"2048x4096": {"1": row(9.0)}}     # another device untouched
+
+
+def test_tuner_candidate_sets(monkeypatch):
+    """Refine times the current table entry first, then only stage-3 and split tiles, all of
+    them built for the shape; the split is offered only where the unsplit tiles are few;
+    `capture` is vLLM's graph batch sizes."""
+    import json
+
+    from int8_linear import tune
+    from int8_linear.kernel import tuned_config
+    shipped = json.loads(kernel.TUNED_PATH.read_text())["gfx950"]
+    monkeypatch.setattr(kernel.torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(kernel, "_device_table", lambda dev: shipped)
+    m, k, n = 64, 14336, 4096                                # Llama-3-8B down_proj
+    assert tuned_config(m, n, k) is not None
+    ref = tune.refine_candidates(m, k, n)
+    assert ref[0] == (tuned_config(m, n, k) or default_config(m, n, k))
+    assert len(set(ref)) == len(ref)
+    split = lambda c: c.stages == 5 and c.bn <= 64          # wider stage-5 tiles: prefill rings
+    assert all(c.stages in (3, 5) and c.bn <= 64 for c in ref[1:]) and any(map(split, ref))
+    assert all(kernel.supported(m, n, k, c) for c in ref)
+    full = tune.candidate_configs(m, k, n)
+    assert set(ref[1:]) <= set(full) and len(full) > len(ref)
+    for mm, kk, nn in ((m, k, n), (16, 4096, 28672), (1, 2048, 12288), (128, 4096, 28672)):
+        for c in filter(split, tune.candidate_configs(mm, kk, nn)):
+            tiles = -(-mm // c.bm) * (nn // c.bn)
+            assert tiles < 512 and tiles * c.group_m <= 1024, (mm, c.name)
+    # 128 tokens on Llama-3-8B gate_up: every split tile already has 512 or more tiles
+    assert not any(map(split, tune.candidate_configs(128, 4096, 28672)))
+    assert tune.parse_ms("capture") == list(tune.CAPTURE_SIZES)
+    assert tune.parse_ms("1,2,17") == [1, 2, 17]
