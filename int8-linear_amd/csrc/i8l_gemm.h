@@ -38,9 +38,13 @@ __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) 
   return ((const float*)bias)[n];
 }
 
-// Per-column epilogue operands of four consecutive output columns n..n+3.
+// Per-column epilogue operands of four consecutive output columns n..n+3.  A 16-bit bias is
+// kept as loaded (hb: four bf16/fp16 values) and widened where the epilogue adds it: widening
+// at the load would make the compiler wait for that load (and for every memory request
+// issued before it, such as the current weight copy) before the next copy is requested.
 struct Cols4 {
   float sb[4], bias[4];
+  uint2 hb;
 };
 
 // Epilogue kinds.  EK_ANY reads the output dtype, the bias dtype and the scale layout from
@@ -85,11 +89,7 @@ __device__ __forceinline__ Cols4 load_cols4(const Epi& e, int64_t n) {
     const float4 v = *(const float4*)((const float*)e.bias + n);
     c.bias[0] = v.x, c.bias[1] = v.y, c.bias[2] = v.z, c.bias[3] = v.w;
   } else if (bd == I8L_BF16 || bd == I8L_F16) {
-    const uint2 h = *(const uint2*)((const uint16_t*)e.bias + n);
-    const uint32_t w[4] = {h.x & 0xffffu, h.x >> 16, h.y & 0xffffu, h.y >> 16};
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      c.bias[r] = bd == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
+    c.hb = *(const uint2*)((const uint16_t*)e.bias + n);   // widened in store4s
   } else {
     c.bias[0] = c.bias[1] = c.bias[2] = c.bias[3] = 0.0f;
   }
@@ -112,13 +112,23 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
     *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
     return;
   }
+  float bias[4];
+  if (bd == I8L_BF16 || bd == I8L_F16) {
+    const uint32_t w[4] = {c.hb.x & 0xffffu, c.hb.x >> 16, c.hb.y & 0xffffu, c.hb.y >> 16};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bias[r] = bd == I8L_BF16 ? bf16_bits_to_f32(w[r]) : f16_bits_to_f32(w[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[r] = c.bias[r];
+  }
   float o[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float v = (float)acc[r];
     v = v * sam;
     v = v * c.sb[r];
-    if (bd != I8L_DTYPE_NONE) v = v + c.bias[r];
+    if (bd != I8L_DTYPE_NONE) v = v + bias[r];
     o[r] = v;
   }
   if (od == I8L_F32) {
