@@ -82,8 +82,7 @@ __device__ __forceinline__ Cols4 load_cols4(const Epi& e, int64_t n) {
     const float4 v = *(const float4*)(e.sb + n);
     c.sb[0] = v.x, c.sb[1] = v.y, c.sb[2] = v.z, c.sb[3] = v.w;
   } else {
-    const float v = e.sb[0];
-    c.sb[0] = c.sb[1] = c.sb[2] = c.sb[3] = v;
+    c.sb[0] = e.sb[0];   // one scale for every column: store4s reads sb[0] (no copies here)
   }
   if (bd == I8L_F32) {
     const float4 v = *(const float4*)((const float*)e.bias + n);
@@ -127,7 +126,7 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
   for (int r = 0; r < 4; ++r) {
     float v = (float)acc[r];
     v = v * sam;
-    v = v * c.sb[r];
+    v = v * (epi_sb_per_col<EK>(e) ? c.sb[r] : c.sb[0]);
     if (bd != I8L_DTYPE_NONE) v = v + bias[r];
     o[r] = v;
   }
