@@ -245,6 +245,7 @@ inline void lds_opt_in(const void* kern, size_t bytes, std::atomic<uint64_t>& do
 
 // ------------------------------------------------------------------ schedules (host side)
 // Decode (i8l_gemm_decode.hip).
+int cu_count();   // compute units of the current device, 256 without one
 bool stream_ok(const i8l_config& c);
 bool wlds_ok(const i8l_config& c, int64_t K);
 bool wlds_split_ok(const i8l_config& c, int64_t K);

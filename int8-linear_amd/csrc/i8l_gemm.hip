@@ -95,20 +95,38 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
       }
     }
   }
-  // Mid batches on wide or many-token problems: 64-token tiles of 128 columns with the
-  // direct-to-LDS ring; the activations are re-read N/128 times instead of N/32.
-  // 129 to 1024 tokens, and from 33 tokens on wide N: the largest of the 4-wave overlapped-
-  // ring tiles (128x128, 128x64, 64x128, 64x64) that still gives every CU a workgroup, else
-  // the smallest.  At these sizes the per-CU latency of the K loop, not the MFMA rate, sets
-  // the time, so more workgroups beat fewer re-reads.
-  if (M <= 1024 && N % 64 == 0 && K % 128 == 0 && (M > 128 || (M > 32 && N >= 8192))) {
-    const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-    for (const auto& t : tiles)
-      if (N % t[1] == 0 && ((M + t[0] - 1) / t[0]) * (N / t[1]) >= 256) {
-        *c = i8l_config{t[0], t[1], 128, 4, 4 + kPipelined, 8};
-        return;
+  // 129 tokens and more, and from 33 tokens on wide N (K a multiple of 128): the overlapped-
+  // ring tile with the least (waves of workgroups, one a CU) x (one wave's time).  kRing holds
+  // each tile's time for one wave, relative to the 64x64 tile's 2.08 ns per K byte, the
+  // median over 15 weight shapes (K 2048-28672, N 2048-57344) at 48-4096 tokens on MI355X.
+  // Small tiles win while there are few tokens (more workgroups), large ones once every tile
+  // size fills the CUs (fewer operand re-reads); a last wave of a few workgroups costs as much
+  // as a full one, and of two tiles within 1% of each other the one with fewer waves wins
+  // (each wave boundary drains the ring).  Over those shapes the pick was within 9% of the
+  // fastest of these tiles, 0.2% on the geometric mean (the costs fitted on half the shapes
+  // picked within 1.2% on the other half).
+  struct RingTile {
+    int bm, bn, warps, stages, group_m, cost;
+  };
+  static constexpr RingTile kRing[] = {
+      {64, 64, 4, 4 + kPipelined, 8, 100},   {128, 64, 4, 4 + kPipelined, 8, 165},
+      {64, 128, 4, 4 + kPipelined, 8, 178},  {128, 128, 4, 4 + kPipelined, 8, 249},
+      {64, 256, 8, 3 + kPipelined, 8, 285},  {256, 128, 8, 3 + kPipelined, 8, 369},
+      {128, 256, 8, 3 + kPipelined, 8, 384}, {256, 192, 8, 2 + kPipelined, 4, 555},
+      {256, 256, 8, 2 + kPipelined, 4, 570}};
+  if (K % 128 == 0 && N % 64 == 0 && (M > 128 || (M > 32 && N >= 8192))) {
+    const int64_t cus = cu_count();
+    int64_t best = -1, best_waves = 0;
+    for (const auto& t : kRing) {
+      if (N % t.bn != 0) continue;
+      const int64_t waves = (((M + t.bm - 1) / t.bm) * (N / t.bn) + cus - 1) / cus;
+      const int64_t cost = t.cost * waves;
+      if (best < 0 || cost * 100 < best * 99 || (cost * 100 <= best * 101 && waves < best_waves)) {
+        best = cost;
+        best_waves = waves;
+        *c = i8l_config{t.bm, t.bn, 128, t.warps, t.stages, t.group_m};
       }
-    *c = i8l_config{64, 64, 128, 4, 4 + kPipelined, 8};
+    }
     return;
   }
   // 17 to 128 tokens: weights through LDS in 32-token x 32-column tiles (several row
@@ -138,17 +156,12 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     c->stages = 1;
     return;
   }
-  // Prefill: direct-to-LDS macro tiles with the fragment reads overlapped with the MFMAs
-  // (the fastest measured family on MI355X): 256x256 tiles once there are enough of them
-  // (with 128-byte K steps, whole cache lines, in a double buffer when K allows), 128x128
-  // tiles (more workgroups) below.
+  // Prefill with K not a multiple of 128 (or N not of 64): direct-to-LDS macro tiles with the
+  // fragment reads overlapped with the MFMAs, 256x256 in 64-byte K steps when N allows,
+  // 128x128 tiles below.
   c->group_m = 8;
-  if (N % 256 == 0 && K % 128 == 0 && M > 1024) {
-    *c = i8l_config{256, 256, 128, 8, 10, 4};
-  } else if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
+  if (N % 256 == 0 && K % 64 == 0 && M > 1024) {
     *c = i8l_config{256, 256, 64, 8, 12, 4};
-  } else if (N % 128 == 0 && K % 128 == 0) {
-    *c = i8l_config{128, 128, 128, 4, 12, 8};
   } else if (N % 128 == 0 && K % 64 == 0) {
     *c = i8l_config{128, 128, 64, 4, 12, 8};
   } else {

@@ -81,8 +81,9 @@ def _cconfig(cfg: Config) -> _lib.CConfig:
 
 def default_config(m: int, n: int, k: int) -> Config:
     """The untuned choice (the library's own rule, i8l_default_config): weights through LDS
-    up to 32 tokens, 64x128 overlapped-ring tiles for wide N up to 128 tokens and for any N
-    up to 512, weight streaming otherwise up to 128 tokens, prefill macro tiles above."""
+    up to 32 tokens (the persistent tile on many column tiles), 32x32 weights-through-LDS
+    tiles up to 128 tokens below N = 8192, and above that the overlapped-ring tile (64x64
+    up to 256x256) with the least waves of workgroups times one wave's measured time."""
     c = _lib.CConfig()
     _lib.check(_lib.lib().i8l_default_config(m, n, k, c), NotSupported)
     return Config(c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m)

@@ -58,11 +58,19 @@ def test_default_config_regimes():
     assert default_config(16, 28672, 4096) == Config(16, 8, 512, 8, 4, 2)
     assert default_config(4, 12288, 2048).stages == 3     # few tokens: A is small
     assert default_config(24, 28672, 4096).stages == 3    # no 32-row 8-column persistent tile
-    mid = default_config(96, 12288, 2048)                   # 64-token overlapped-ring tiles
-    assert (mid.bm, mid.bn, mid.stages) == (64, 64, 12)
-    assert (default_config(512, 4096, 4096).bm, default_config(512, 4096, 4096).bn) == (128, 64)
-    assert (default_config(1024, 4096, 4096).bm, default_config(1024, 4096, 4096).bn) == (128, 128)
-    assert default_config(400, 2048, 6144).bm == 64
+    # From 129 tokens (33 on wide N) the overlapped-ring tile with the least waves x wave
+    # time, one workgroup a CU on a 256-CU part: small tiles while few tokens leave CUs idle,
+    # the largest tile that still fills one wave once it does.
+    bmn = lambda m, n, k: (default_config(m, n, k).bm, default_config(m, n, k).bn)
+    assert default_config(96, 12288, 2048) == Config(128, 64, 128, 4, 12, 8)
+    assert bmn(512, 4096, 4096) == (128, 64)              # 256 tiles of 128x64 (one wave)
+    assert bmn(1024, 4096, 4096) == (128, 128)            # 256 tiles of 128x128
+    assert bmn(400, 2048, 6144) == (64, 64)               # 224 tiles: anything larger idles CUs
+    assert bmn(272, 6144, 4096) == (64, 128)              # 240 of 64x128 beat 288 of 128x64
+    assert default_config(288, 12288, 2048) == Config(64, 256, 128, 8, 11, 8)
+    assert default_config(400, 28672, 4096) == Config(256, 256, 128, 8, 10, 4)
+    assert bmn(2048, 2048, 2048) == (128, 128)            # 256x256 would leave 3/4 of the CUs idle
+    assert bmn(2048, 4096, 4096) == (256, 128)
     assert default_config(96, 4096, 2048).bn == 32          # narrower N: 32-column tiles
     for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
         assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
