@@ -81,40 +81,80 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int T = 64 * WM * WN;
   const int frow = lane & 31, fhalf = lane >> 5;
-  if (e.out_dtype == I8L_I32 || e.out_dtype == I8L_F32) {
+  const bool out4 = e.out_dtype == I8L_I32 || e.out_dtype == I8L_F32;
+  float sam[FB];
+  Cols4 cls[FA][4];
+  if (e.out_dtype != I8L_I32) {
 #pragma unroll
-    for (int a = 0; a < FA; ++a)
+    for (int b = 0; b < FB; ++b) {
+      const int64_t m = m0 + wm * TM + b * 32 + frow;
+      sam[b] = load_sa(e, m < e.M ? m : 0);
+    }
+    if (e.sb_per_col)
+      load_tile_cols_s<FA, true>(e, n0 + wn * TN + 4 * fhalf, cls);
+    else
+      load_tile_cols_s<FA, false>(e, n0 + wn * TN + 4 * fhalf, cls);
+  }
+  // The value of element (a, b, q, i) before its cast: acc * scale_a * scale_b + bias in
+  // fp32, left to right (a missing bias is -0, the identity of the addition).
+  auto value = [&](int a, int b, int q, int i) {
+    float v = (float)acc[a][b][4 * q + i];
+    v = v * sam[b];
+    v = v * cls[a][q].sb[i];
+    return v + cls[a][q].bias[i];
+  };
+  if (out4) {
+    // 4-byte outputs (int32 raw, fp32): staged through LDS half the tile's rows at a time
+    // (BM/2 rows of 4*BN bytes fit the area of the 16-bit staging) and written in whole
+    // 16-byte chunks by consecutive lanes, as the 16-bit outputs are.  A wave's TM rows lie
+    // in one half (WM is even).
+    static_assert(WM % 2 == 0, "a wave's rows must lie in one half of the tile");
+    constexpr int HR = BM / 2;
+    constexpr int PITCH4 = 4 * BN + 16;
+    constexpr int CPR4 = BN / 4;                 // 16-byte chunks per output row
+    static_assert((HR * CPR4) % T == 0, "half-tile rows do not split over the threads");
+    const bool raw = e.out_dtype == I8L_I32;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wn * TN + a * 32 + 8 * q + 4 * fhalf;
-        Cols4 cl = load_cols4(e, n);
+    for (int h = 0; h < 2; ++h) {
+      if ((wm * TM) / HR == h) {
 #pragma unroll
-        for (int b = 0; b < FB; ++b) {
-          const int64_t m = m0 + wm * TM + b * 32 + frow;
-          const v4i v = {acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2],
-                         acc[a][b][4 * q + 3]};
-          if (m < e.M) store4c(e, m, n, v, cl);
-        }
+        for (int a = 0; a < FA; ++a)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int c = wn * TN + a * 32 + 8 * q + 4 * fhalf;
+#pragma unroll
+            for (int b = 0; b < FB; ++b) {
+              const int r = wm * TM + b * 32 + frow - h * HR;
+              v4i v;
+              if (raw) {
+                v = v4i{acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2],
+                        acc[a][b][4 * q + 3]};
+              } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = __float_as_int(value(a, b, q, i));
+              }
+              *(v4i*)(lds + r * PITCH4 + 4 * c) = v;
+            }
+          }
       }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < HR * CPR4 / T; ++j) {
+        const int i = tid + j * T;
+        const int r = i / CPR4, c4 = i % CPR4;
+        const int64_t m = m0 + h * HR + r;
+        const v4i v = *(const v4i*)(lds + r * PITCH4 + 16 * c4);
+        if (m < e.M) __builtin_nontemporal_store(v, (v4i*)((int32_t*)e.out + m * e.ldc + n0 + 4 * c4));
+      }
+      if (h == 0) __syncthreads();   // the second half reuses the area
+    }
     return;
   }
   constexpr int PITCH = 2 * BN + 16;  // bytes per LDS row (16-byte aligned)
-  float sam[FB];
-#pragma unroll
-  for (int b = 0; b < FB; ++b) {
-    const int64_t m = m0 + wm * TM + b * 32 + frow;
-    sam[b] = load_sa(e, m < e.M ? m : 0);
-  }
-  Cols4 cls[FA][4];
-  if (e.sb_per_col)
-    load_tile_cols_s<FA, true>(e, n0 + wn * TN + 4 * fhalf, cls);
-  else
-    load_tile_cols_s<FA, false>(e, n0 + wn * TN + 4 * fhalf, cls);
   // the output dtype is uniform: one copy of the conversion loop per dtype, no per-value select
   auto stage = [&](auto pack2) {
 #pragma unroll
     for (int a = 0; a < FA; ++a) {
-      const Cols4 (&cl)[4] = cls[a];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = wn * TN + a * 32 + 8 * q + 4 * fhalf;  // column within the tile
@@ -123,12 +163,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, v16i (&acc)[FA][FB],
           const int r = wm * TM + b * 32 + frow;             // row within the tile
           float v[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[i] = (float)acc[a][b][4 * q + i];
-            v[i] = v[i] * sam[b];
-            v[i] = v[i] * cl[q].sb[i];
-            v[i] = v[i] + cl[q].bias[i];
-          }
+          for (int i = 0; i < 4; ++i) v[i] = value(a, b, q, i);
           *(uint2*)(lds + r * PITCH + 2 * c) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
         }
       }

@@ -128,20 +128,29 @@ def _prefill_tiles():
 @pytest.mark.parametrize("m,n", [(700, 2304), (300, 4608)])
 def test_every_prefill_tile_is_repeatable(m, n):
     """Every prefill tile the tuner may pick, called 20 times in a row at a shape where two
-    workgroups share a CU, gives the same bits each time and the oracle's bits."""
+    workgroups share a CU, gives the same bits each time and the oracle's bits; and its
+    4-byte outputs (raw int32, fp32), which are staged through LDS in two halves of the
+    tile's rows, give the oracle's values on every one of 5 calls."""
     k = 2048
     say(f"w8a8_mm every prefill tile repeated m={m} k={k} n={n}")
     a, w = ints((m, k), 13), ints((n, k), 14)
     sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
     sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    one = torch.ones(1, device="cuda")
     want = oracle_out(a, w, sa, sb, None, torch.bfloat16)
+    want_f32 = oracle_out(a, w, sa, sb, None, torch.float32)
+    want_i32 = o.gemm_i32(np_(a), np_(w))
     for config in _prefill_tiles():
         if not kernel.supported(m, n, k, config):
             continue
         outs = [w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=config) for _ in range(20)]
+        raws = [w8a8_mm(a, w.t(), one, one, raw=True, config=config) for _ in range(5)]
+        f32s = [w8a8_mm(a, w.t(), sa, sb, torch.float32, config=config) for _ in range(5)]
         torch.cuda.synchronize()
         assert np.array_equal(bits(outs[0]), want), config.name
         assert all(torch.equal(o, outs[0]) for o in outs), config.name
+        assert all(np.array_equal(np_(r), want_i32) for r in raws), config.name
+        assert all(np.array_equal(np_(f), want_f32) for f in f32s), config.name
 
 
 @pytest.mark.parametrize("m", [16, 100])
