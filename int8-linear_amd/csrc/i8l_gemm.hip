@@ -144,13 +144,17 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
       return;
     }
   }
+  // N not a multiple of 16: the 8-column (at most 32-token) or 4-column (16-token) streaming
+  // tiles, several row blocks if M needs them.
+  const int sbn = N % 16 == 0 ? 16 : N % 8 == 0 ? 8 : 4;
+  const int smt_max = sbn == 16 ? 8 : sbn == 8 ? 2 : 1;
   if (M <= 128) {
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    const int mt = std::min(M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8, smt_max);
     // enough waves that each owns only a few 64-byte K steps, as many as fit a workgroup
     int W = stream_max_threads(mt, 1) / 64;
     while (W > 1 && (K % (64 * W) != 0 || K / (64 * W) < 4 || W * mt * 1024 > 96 * 1024)) W /= 2;
     c->bm = 16 * mt;
-    c->bn = 16;
+    c->bn = sbn;
     c->warps = W;
     c->bk = 64 * W;
     c->stages = 1;
@@ -166,9 +170,10 @@ void default_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
     *c = i8l_config{128, 128, 64, 4, 12, 8};
   } else {
     // narrow or odd shapes: the weight-streaming tile, one 128-token row block at a time
-    int W = stream_max_threads(8, 1) / 64;
+    // (32 or 16 tokens for N not a multiple of 16)
+    int W = stream_max_threads(smt_max, 1) / 64;
     while (W > 1 && K % (64 * W) != 0) W /= 2;
-    *c = i8l_config{128, 16, 64 * W, W, 1, 1};
+    *c = i8l_config{16 * smt_max, sbn, 64 * W, W, 1, 1};
   }
 }
 

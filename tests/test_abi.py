@@ -47,8 +47,10 @@ def test_default_config_regimes():
     s = default_config(64, 4096, 2048)                      # 32x32 tiles through LDS
     assert (s.bm, s.bn, s.stages, s.warps) == (32, 32, 3, 16)
     assert (default_config(128, 2048, 6144).bk, default_config(128, 2048, 6144).warps) == (256, 4)
-    s = default_config(64, 4104, 2056)                      # odd K: register-streamed weights
+    s = default_config(64, 4096, 2056)                      # odd K: register-streamed weights
     assert s.stages == 1 and s.bm == 64 and s.bk == 64 * s.warps
+    s = default_config(64, 4104, 2048)                      # N = 8 mod 16: 8-column stream tiles
+    assert (s.stages, s.bm, s.bn) == (1, 32, 8) and kernel.supported(64, 4104, 2048, s)
     p = default_config(4096, 28672, 4096)
     assert p.stages >= 2 and (p.bm, p.bn) == (256, 256)
     assert default_config(300, 2048, 2048).stages >= 2
@@ -74,6 +76,19 @@ def test_default_config_regimes():
     assert default_config(96, 4096, 2048).bn == 32          # narrower N: 32-column tiles
     for m, n, k in ((300, 2048, 2048), (4096, 4096, 14336), (700, 6144, 4096), (200, 48, 256)):
         assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
+
+
+def test_default_config_takes_every_aligned_shape():
+    """The library default is a built, supported configuration for every M and every N, K
+    the fast schedules can take (N a multiple of 4, K of 64): narrow N included, where it
+    falls back to 8- or 4-column streaming tiles."""
+    ms = (1, 7, 16, 17, 32, 33, 64, 65, 128, 129, 300, 512, 1025, 4096, 16384)
+    ks = (64, 192, 640, 2048, 2112, 5120, 14336)
+    ns = (4, 8, 12, 24, 40, 48, 96, 320, 2304, 6144, 57344)
+    for m in ms:
+        for k in ks:
+            for n in ns:
+                assert kernel.supported(m, n, k, default_config(m, n, k)), (m, n, k)
 
 
 def test_every_tuner_candidate_tile_is_built():

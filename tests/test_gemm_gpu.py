@@ -334,6 +334,19 @@ def test_scaled_output_matches_oracle_and_float64(m, dtype, per_row, per_col, bi
         assert np.all(np.abs(np_(got.float()).astype(np.float64) - ref) <= ulp)
 
 
+@pytest.mark.parametrize("m,n", [(5, 24), (40, 8), (100, 40), (300, 24), (1500, 12)])
+def test_default_config_narrow_n(m, n):
+    """N not a multiple of 16 takes the library default's 8- or 4-column streaming tiles."""
+    k = 2112
+    say(f"w8a8_mm default narrow N m={m} n={n} k={k}")
+    a, w = ints((m, k), 51), ints((n, k), 52)
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    assert kernel.default_config(m, n, k).bn == (8 if n % 8 == 0 else 4)
+    out = w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=kernel.default_config(m, n, k))
+    assert np.array_equal(bits(out), oracle_out(a, w, sa, sb, None, torch.bfloat16))
+
+
 def test_declines_shapes_the_tiles_do_not_divide():
     a, w = ints((4, 100), 8), ints((64, 100), 9)
     one = torch.ones(1, device="cuda")
