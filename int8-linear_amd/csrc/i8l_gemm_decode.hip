@@ -291,7 +291,8 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     const int64_t ko = (int64_t)step * S;
 #pragma unroll
     for (int t = 0; t < NI; ++t)
-      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0,
+                                       kWeightCpol);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -432,7 +433,11 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
     const int64_t ko = (int64_t)step * S;
 #pragma unroll
     for (int t = 0; t < NI; ++t)
-      __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
+      if (t * 1024 + 1023 < NC * S)   // weight rows only: streamed
+        __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0,
+                                         kWeightCpol);
+      else                            // activation rows, which other workgroups re-read
+        __builtin_amdgcn_global_load_lds((const void*)(gsrc[t] + ko), dst + t * 1024, 16, 0, 0);
     if (fenced) __builtin_amdgcn_sched_barrier(0);
   };
   auto compute = [&](int step) {
@@ -515,7 +520,7 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
     const int o = t * 1024 + 16 * lane;
     const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
     __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
-                                     16, 0, 0);
+                                     16, 0, kWeightCpol);
   }
   const int8_t* Aw = A + m0 * lda + kw + 16 * grp;
   const int lda32 = (int)lda;
@@ -622,7 +627,7 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
       const int o = t * 1024 + 16 * lane;
       const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
       __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
-                                       16, 0, 0);
+                                       16, 0, kWeightCpol);
     }
   };
 
@@ -776,7 +781,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
     const int o = t * 1024 + 16 * lane;
     const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
     __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
-                                     16, 0, 0);
+                                     16, 0, kWeightCpol);
   }
   __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt_wlds<NI>();  // vector loads complete in issue order: the activations are in
