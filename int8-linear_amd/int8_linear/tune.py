@@ -195,8 +195,15 @@ def refine_candidates(m: int, k: int, n: int) -> list[Config]:
     return [cur] + [c for c in new if c != cur]
 
 
-def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = False) -> dict:
-    """{str(M): {"config": {...}, "graph_us": t, "default_us": t0}} for one weight shape."""
+def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = False,
+               min_gain: float = 0.0) -> dict:
+    """{str(M): {"config": {...}, "graph_us": t, "default_us": t0}} for one weight shape.
+
+    The configuration the stored table gives now (tuned_config) is always among the
+    finalists, and a row with one also records its time as "table_us"; with min_gain > 0 the
+    stored configuration is kept unless the best finalist is that fraction faster, so that
+    re-tuning a table does not trade entries on timing noise."""
+    from int8_linear.kernel import tuned_config
     d = operands(16, k, n, seed_of(16, k, n), device=device)
     copies = max(2, -(-ROTATE_BYTES // (k * n)))
     ws = [d["w_q"]] + [d["w_q"].clone() for _ in range(copies - 1)]
@@ -223,18 +230,28 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = 
         # of their timings wins.
         timed.sort(key=lambda t: t[0])
         finals = {c: [us] for us, c in timed[:FINALISTS]}
+        cur = tuned_config(m, n, k)
+        if cur is not None and cur not in finals and supported(m, n, k, cur):
+            finals[cur] = [next((us for us, c in timed if c == cur), None) or time_cold_us(
+                lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16,
+                                  config=cur), copies)]
         for _ in range(FINAL_ROUNDS):
             for c in finals:
                 finals[c].append(time_cold_us(lambda i, c=c: w8a8_mm(
                     a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16, config=c), copies))
-        best = min(((statistics.median(v), c) for c, v in finals.items()), key=lambda t: t[0])
-        best = (best[1], best[0])
+        med = {c: statistics.median(v) for c, v in finals.items()}
+        best = min(med.items(), key=lambda t: t[1])
+        if cur in med and best[1] > med[cur] * (1.0 - min_gain):
+            best = (cur, med[cur])
         if t0 is None:
             t0 = time_cold_us(lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16,
                                                 config=default_config(m, n, k)), copies)
-        log(f"K={k} N={n} M={m}: best {best[0].name} {best[1]:.2f} us (default {t0:.2f} us)")
+        table = f", table {cur.name} {med[cur]:.2f} us" if cur in med else ""
+        log(f"K={k} N={n} M={m}: best {best[0].name} {best[1]:.2f} us (default {t0:.2f} us{table})")
         rows[str(m)] = {"config": asdict(best[0]), "graph_us": round(best[1], 3),
                         "default_us": round(t0, 3)}
+        if cur in med:
+            rows[str(m)]["table_us"] = round(med[cur], 3)
     del ws
     torch.cuda.empty_cache()
     return rows
@@ -261,6 +278,9 @@ def main() -> int:
     ap.add_argument("--refine", action="store_true",
                     help="time only the current table entry against the weights-through-LDS "
                          "tiles and the split of K (stages 3 and 5)")
+    ap.add_argument("--min-gain", type=float, default=0.0,
+                    help="keep the stored entry unless a candidate is this fraction faster "
+                         "(e.g. 0.02)")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
     dev = torch.device("cuda:0")
@@ -272,7 +292,7 @@ def main() -> int:
         if only is not None and f"{k}x{n}" not in only:
             continue
         table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True),
-                                       refine=args.refine)
+                                       refine=args.refine, min_gain=args.min_gain)
     if args.out:
         with open(args.out, "w") as f:
             json.dump({arch: table}, f, indent=1)

@@ -44,3 +44,18 @@ def test_tuned_entry_is_bit_exact(k, n, m, cfg):
     acc = o.gemm_i32(np_(d["a_q"]), np_(d["w_q"]))
     ref = o.epilogue(acc, np_(d["a_s"]), np_(d["w_s"]), bits(d["bias"]), o.BF16, o.BF16)
     assert np.array_equal(bits(got), ref)
+
+
+def test_tuner_keeps_the_stored_entry_without_a_clear_gain(monkeypatch):
+    """A re-tune times the stored entry among its finalists and, under --min-gain, keeps it
+    unless a candidate beats it by that fraction (here 99%, which none does)."""
+    from int8_linear import tune
+    k, n, m = 2048, 1024, 16
+    stored = kernel.default_config(m, n, k)
+    say(f"tune_shape keeps {stored.name} at m={m} k={k} n={n}")
+    monkeypatch.setattr(kernel, "tuned_config", lambda mm, nn, kk: stored)
+    rows = tune.tune_shape(k, n, [m], torch.device("cuda:0"), log=lambda *a: None,
+                           refine=True, min_gain=0.99)
+    row = rows[str(m)]
+    assert Config(**row["config"]) == stored
+    assert row["graph_us"] == row["table_us"] > 0
