@@ -94,7 +94,7 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
         for mt, nc, ks in WLDS_TILES:
             if mt > need:
                 continue  # one row block covering M, or several smaller ones
-            for w in (4, 8, 16):
+            for w in (4, 8, 12, 16):
                 cfg = Config(16 * mt, nc, 64 * ks, w, 3, 1)
                 if supported(m, n, k, cfg):
                     out.append(cfg)

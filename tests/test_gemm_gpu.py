@@ -334,6 +334,29 @@ def test_scaled_output_matches_oracle_and_float64(m, dtype, per_row, per_col, bi
         assert np.all(np.abs(np_(got.float()).astype(np.float64) - ref) <= ulp)
 
 
+@pytest.mark.parametrize("nc", [4, 8, 16])
+@pytest.mark.parametrize("m", [1, 7, 16])
+def test_twelve_wave_tiles(nc, m):
+    """Weights-through-LDS tiles with 12 waves (not a power of two; 256-byte steps, two a
+    wave at K = 6144, a tuner candidate): every epilogue kind, bit-exact against the oracle."""
+    k, n = 6144, 512
+    cfg = Config(16, nc, 256, 12, 3, 1)
+    assert kernel.supported(m, n, k, cfg)
+    say(f"w8a8_mm {cfg.name} m={m} k={k} n={n}")
+    a, w = ints((m, k), 61 + nc), ints((n, k), 62 + m)
+    g = torch.Generator().manual_seed(63)
+    sa = (torch.rand((m, 1), generator=g) * 1e-2 + 1e-3).cuda()
+    sb = (torch.rand((n, 1), generator=g) * 1e-2 + 1e-3).cuda()
+    one = torch.ones(1, device="cuda")
+    assert np.array_equal(np_(w8a8_mm(a, w.t(), one, one, raw=True, config=cfg)),
+                          o.gemm_i32(np_(a), np_(w)))
+    for dtype, bias_dtype in ((torch.bfloat16, None), (torch.bfloat16, torch.bfloat16),
+                              (torch.float32, torch.float16)):
+        bias = torch.randn(n, generator=g).to(bias_dtype).cuda() if bias_dtype else None
+        out = w8a8_mm(a, w.t(), sa, sb, dtype, bias, config=cfg)
+        assert np.array_equal(as_np(out), oracle_out(a, w, sa, sb, bias, dtype)), (dtype, bias_dtype)
+
+
 @pytest.mark.parametrize("m,n", [(5, 24), (40, 8), (100, 40), (300, 24), (1500, 12)])
 def test_default_config_narrow_n(m, n):
     """N not a multiple of 16 takes the library default's 8- or 4-column streaming tiles."""
