@@ -14,19 +14,26 @@ in the 256 MiB Infinity Cache.  `value` is the mean microseconds per linear over
 After the timed steps (not inside them): per-call graph-replay times of every sweep point,
 the roofline object of the dominant kernel (HIP events on the launch stream, algorithmic
 bytes per launch), the fused quantizers (config 2), the prefill shapes (config 3), the
-28-layer decoder stand-in in microseconds per layer (config 4), the CPU baseline (the
-oracle's CPU restatement of the reference's path, on a bounded sample) and, beside it, the
-reference's own CPU path as torch ops (`cpu_reference_path`: torch._int_mm and an int32
-matmul with the fp32 dequant for config 0, the torch quantizers at 1024 tokens), and the
-hardware floors (`floors`: empty-kernel launch, cold HBM reads, sustained int8 MFMA rate)
-measured by probe kernels the same way.
+28-layer decoder stand-in in microseconds per layer (config 4), Llama-3-8B decode, the eager
+host cost per call, the hardware floors measured by probe kernels the same way (empty-kernel
+launch, cold HBM reads, sustained int8 MFMA rate), and on the host cores the CPU baseline:
+the reference's CPU path as torch ops (`cpu_baseline`: torch._int_mm with the fp32 dequant
+for config 0; `cpu_reference_path`: an int32 matmul and the torch quantizers at 1024 tokens)
+and the C oracle (`cpu_oracle`), each on a bounded sample.
 
     python bench.py --roofline-only      # only the config-0 launches (for rocprofv3)
     python bench.py --only standin       # one extra section alone
-                                         # (quant|prefill|standin|launch|llama_decode|floors)
+                         # (quant|prefill|standin|launch|llama_decode|floors|linear)
     python bench.py --only prefill --prefill-m 4096   # config 3 at M=4096 only
-Every GPU output is checked against a float64 reference before it is timed, after the
-output buffer has been poisoned.  Prints ONE JSON line.
+    python bench.py --only linear --kn 14336x4096 --m 64 [--config 32,32,256,4,3,1]
+                         # one linear launched repeatedly, for a profiler to watch
+    python bench.py --details out.json   # also every per-point table, in one file
+
+Every timed output is checked before it is timed, with its output buffer poisoned first:
+the linears against float64, the quantizers and every op of the stand-in against the
+reference's CPU arithmetic.  The last line printed is the one-line JSON result, with only
+scalar fields in each section; the per-point tables are printed on the lines before it
+({"detail": name, "data": ...}).
 """
 
 from __future__ import annotations
@@ -111,6 +118,36 @@ def graph_time_us(fn, calls: int, windows: int = 5) -> float:
     return statistics.median(out)
 
 
+def checked_mm(d, cfg=None, copy=None):
+    """The linear of operand dict d (a_q, w_q [N,K], a_s, w_s, bias) written into an output
+    buffer filled with NaN first: the same C entry point and configuration as the timed calls
+    (i8l_w8a8_mm_ws, cfg or choose_config), with the output passed in, so every element the
+    check reads was written by the kernel (a skipped element stays NaN and fails the check)."""
+    import torch
+
+    from int8_linear import _lib
+    from int8_linear.kernel import _cconfig, choose_config
+    a, w = d["a_q"], d["w_q"] if copy is None else copy
+    m, k = a.shape
+    n = w.shape[0]
+    cfg = cfg or choose_config(m, n, k)
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=a.device)
+    sa, sb = d["a_s"].reshape(-1).contiguous(), d["w_s"].reshape(-1).contiguous()
+    bias = d.get("bias")
+    ws_bytes = _lib.lib().i8l_w8a8_mm_workspace_bytes(m, n, k, _cconfig(cfg))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    st = _lib.lib().i8l_w8a8_mm_ws(
+        a.data_ptr(), a.stride(0), a.stride(1), w.data_ptr(), 1, w.stride(0),
+        sa.data_ptr(), sa.numel(), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None,
+        _lib.BF16 if bias is not None else _lib.DTYPE_NONE,
+        out.data_ptr(), out.stride(0), _lib.BF16, m, n, k,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _cconfig(cfg), _lib.stream_of(a))
+    _lib.check(st, RuntimeError)
+    torch.cuda.synchronize()
+    return out
+
+
 def check_linear(out, d) -> float:
     """Max relative error against float64, relative to max(|ref|, |term|) (reference rule)."""
     import torch
@@ -118,6 +155,134 @@ def check_linear(out, d) -> float:
     ref = term + d["bias"].double() if d["bias"] is not None else term
     scale = torch.maximum(ref.abs(), term.abs()).clamp_min(1e-6)
     return ((out.double() - ref).abs() / scale).max().item()
+
+
+# ---------------------------------------------------------------- output checks
+# The reference's CPU arithmetic, restated in torch ops on the host, checks the quantizer leg
+# and the stand-in before they are timed.  The division is the IEEE one the reference kernel
+# specifies (PRECISE_DIV, int8_linear/fused_quant.py:45-47); the sum of squares, rsqrt and
+# exp are torch's float32 ones, which is why the checks carry the reference test's tolerance
+# (tests/test_fused_quant.py:54-61) rather than bit equality.
+
+def ref_quant(yf):
+    """(codes, scales) of float32 rows: absmax/127 and round(y * 127/absmax), IEEE division
+    (reference fused_quant.py:41-53)."""
+    import torch
+    absmax = yf.abs().amax(-1, keepdim=True)
+    inv = torch.where(absmax == 0, torch.zeros_like(absmax),
+                      torch.full_like(absmax, 127.0) / absmax)
+    return torch.round(yf * inv).clamp(-128, 127).to(torch.int8), absmax / 127.0
+
+
+def ref_norm(x, r, w, eps: float = 1e-6):
+    """add+RMSNorm+quant (reference fused_quant.py:56-73): (codes, scales, residual_out)."""
+    import torch
+    xf = x.float()
+    rout = None
+    if r is not None:
+        xf = xf + r.float()
+        rout = xf.to(x.dtype)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    y = ((xf * torch.rsqrt(var + eps)).to(w.dtype) * w).to(x.dtype)
+    return (*ref_quant(y.float()), rout)
+
+
+def ref_silu(gu, round_silu: bool):
+    """SiLU-and-mul+quant (reference fused_quant.py:76-88): (codes, scales)."""
+    import torch
+    i = gu.shape[1] // 2
+    g, u = gu[:, :i].float(), gu[:, i:].float()
+    a = g / (1.0 + torch.exp(-g))
+    if round_silu:
+        a = a.to(gu.dtype).float()
+    return ref_quant((a * u).to(gu.dtype).float())
+
+
+def ref_mm(q, s, w, ws):
+    """The reference's CPU path of one linear: exact int32 product (torch._int_mm), then
+    acc * scale_a * scale_b in float32 and one cast (kernel.py:105-120)."""
+    import torch
+    acc = torch._int_mm(q, w.t())
+    return (acc.float() * s.reshape(-1, 1) * ws.reshape(1, -1)).to(torch.bfloat16)
+
+
+def check_quant(q, s, q0, s0, what: str) -> None:
+    """The reference test's tolerance (tests/test_fused_quant.py:54-61): codes within one
+    step, at most max(8, 0.1%) of them different, scales within 1e-5 relative."""
+    d = (q.cpu().int() - q0.int()).abs()
+    bad = int(d.ne(0).sum())
+    if d.numel() and (int(d.max()) > 1 or bad > max(8, d.numel() // 1000)):
+        raise SystemExit(f"FAIL {what}: {bad} codes differ, largest by {int(d.max())}")
+    rel = ((s.cpu().float().reshape(-1) - s0.reshape(-1)).abs()
+           / s0.reshape(-1).abs().clamp_min(1e-30)).max().item() if s0.numel() else 0.0
+    if not rel < 1e-5:
+        raise SystemExit(f"FAIL {what}: scales differ by {rel:.3g} relative")
+
+
+def check_standin(stack, rows, h_step) -> int:
+    """Checks the stand-in step the bench times, h_step being its output (the last down_proj
+    output of the captured graph's replay):
+      * an eager run of the same chain with every op launched on its own (the folded kernels
+        are bit-identical to the launches they replace) ends in h_step bit for bit;
+      * along that run, each op's output on the token rows `rows`, computed on the host from
+        that op's own GPU inputs in the reference's CPU arithmetic: the GEMMs (exact int32
+        product, fp32 dequant, one cast) and the residual adds bit for bit, the quantizers
+        within the reference test's tolerance.  (Every op works on each token row alone.)
+    Checking op by op rather than the chain's end: one code that rounds the other way early in
+    28 layers moves the end by a few percent, so only per-op checks have a tight bar.
+    Returns the number of ops checked."""
+    import torch
+
+    from int8_linear import fused_quant as fq
+    from int8_linear.kernel import w8a8_mm
+    from int8_linear.standin import EPS, Q_COLS
+    gamma = stack.norm.cpu()
+    ops = 0
+
+    def rows_of(t):
+        return t[rows].cpu()
+
+    def norm(x, r):
+        nonlocal ops
+        q, s, rout = fq.add_rmsnorm_quant(x, r, stack.norm, EPS, fq.PRECISE_DIV)
+        q0, s0, r0 = ref_norm(rows_of(x), rows_of(r) if r is not None else None, gamma, EPS)
+        check_quant(rows_of(q), rows_of(s), q0, s0, f"stand-in add_rmsnorm_quant layer {i}")
+        if r is not None and not torch.equal(rows_of(rout), r0):
+            raise SystemExit(f"FAIL stand-in residual add layer {i}")
+        ops += 1
+        return q, s, rout
+
+    def mm(name, q, s):
+        nonlocal ops
+        w, ws = stack.layers[i][name]
+        out = w8a8_mm(q, w.t(), s, ws, torch.bfloat16, config=stack.configs.get(name))
+        if not torch.equal(rows_of(out), ref_mm(rows_of(q), rows_of(s), w.cpu(), ws.cpu())):
+            raise SystemExit(f"FAIL stand-in {name} layer {i}")
+        ops += 1
+        return out
+
+    res = stack.x
+    i = 0
+    q, s, _ = norm(stack.x, None)
+    h = None
+    for i in range(len(stack.layers)):
+        if i:
+            q, s, res = norm(h, res)
+        a = mm("qkv_proj", q, s)
+        q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
+        q0, s0 = ref_quant(rows_of(a[:, :Q_COLS]).float())
+        check_quant(rows_of(q), rows_of(s), q0, s0, f"stand-in quant_per_token layer {i}")
+        h = mm("o_proj", q, s)
+        q, s, res = norm(h, res)
+        gu = mm("gate_up_proj", q, s)
+        q, s = fq.silu_mul_quant(gu, fq.PRECISE_DIV, fq.ROUND_SILU)
+        q0, s0 = ref_silu(rows_of(gu), fq.ROUND_SILU)
+        check_quant(rows_of(q), rows_of(s), q0, s0, f"stand-in silu_mul_quant layer {i}")
+        h = mm("down_proj", q, s)
+        ops += 2
+    if not torch.equal(h, h_step):
+        raise SystemExit("FAIL stand-in: the timed graph's output differs from the op-by-op run")
+    return ops
 
 
 class Sweep:
@@ -351,13 +516,20 @@ def main() -> int:
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
     ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch", "llama_decode",
-                                       "floors"],
+                                       "floors", "linear"],
                     default=None,
                     help="run one extra section alone (for profiling) and print its JSON")
     ap.add_argument("--calibrate", action="store_true",
                     help="with --only: also run three 256 MiB device copies (counter scale)")
     ap.add_argument("--prefill-m", type=int, nargs="+", default=None,
                     help="with --only prefill: the token counts to run (default 512-4096)")
+    ap.add_argument("--details", default=None,
+                    help="also write the result with every per-point table to this JSON file")
+    ap.add_argument("--kn", default=None, help="with --only linear: K x N of the weight")
+    ap.add_argument("--m", type=int, default=None, help="with --only linear: tokens")
+    ap.add_argument("--config", default=None,
+                    help="with --only linear: bm,bn,bk,warps,stages,group_m (default: the "
+                         "library's choice)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
@@ -379,7 +551,8 @@ def main() -> int:
     if args.only:
         fn = {"quant": bench_quant, "prefill": lambda d: bench_prefill(d, args.prefill_m),
               "standin": bench_standin, "launch": bench_launch,
-              "llama_decode": bench_llama_decode, "floors": bench_floors}[args.only]
+              "llama_decode": bench_llama_decode, "floors": bench_floors,
+              "linear": lambda d: run_linear(d, args.kn, args.m, args.config)}[args.only]
         res = {args.only: fn(dev)}
         if args.calibrate:
             res["calibration"] = copy_calibration(dev)
@@ -389,15 +562,17 @@ def main() -> int:
     sw = Sweep(shapes, DECODE_M, dev)
     log(f"sweep: {len(sw.points)} linears, weight copies per shape {sorted(sw.copies.values())}")
 
-    # correctness first, into poisoned outputs
+    # correctness first: each point through the C entry into a poisoned output, checked
+    # against float64, and the timed call path (the binding) must give the same bits
     worst = 0.0
     for i, (label, m, k, n, bias, d) in enumerate(sw.points):
-        torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=dev)
-        out = sw.call(i, 0)
+        out = checked_mm(d)
         err = check_linear(out, d)
         worst = max(worst, err)
         if not err <= 1e-2:
             raise SystemExit(f"FAIL: {label} M={m} bias={bias}: max rel err {err}")
+        if not torch.equal(sw.call(i, 0), out):
+            raise SystemExit(f"FAIL: {label} M={m} bias={bias}: the timed path differs")
     log(f"sweep checked against float64: worst rel err {worst:.3g}")
 
     # one step = the whole sweep, each call on its own weight copy, one graph (two graphs
@@ -441,14 +616,13 @@ def main() -> int:
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8xint8->int32, bf16 out", "data": "synthetic",
-        "config": {"workload": "BASELINE config 1: decode sweep, Qwen3-1.7B vLLM shapes "
-                               "(qkv 2048->4096, o 2048->2048, gate_up 2048->12288, "
-                               "down 6144->2048) x M{1,2,4,8,16,17,32,64,128} x bias{off,on}",
+        "config": {"workload": "BASELINE config 1: decode sweep, 4 Qwen3-1.7B linears x "
+                               "M{1,2,4,8,16,17,32,64,128} x bias{off,on}",
                    "linears_per_step": n_calls,
-                   "weight_copies": {f"{k}x{n}": c for (k, n), c in sw.copies.items()},
                    "min_reuse_MiB": round(sw.min_reuse_bytes(plan) / 2 ** 20, 1),
                    "sweep_GBps": round(sweep_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
     }
+    details = {"weight_copies": {f"{k}x{n}": c for (k, n), c in sw.copies.items()}}
 
     result["roofline"] = roofline_config0(dev)
     log(f"roofline config0: {result['roofline']['avg_launch_us']:.2f} us, "
@@ -460,25 +634,115 @@ def main() -> int:
             us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies[(k, n)], windows=3)
             gbs = gemm_bytes(m, k, n, bias) / (us * 1e-6) / 1e9
             table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
-        result["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
-        result["quant"] = bench_quant(dev)
-        result["llama_decode"] = bench_llama_decode(dev)
-        result["prefill"] = bench_prefill(dev)
-        result["standin"] = bench_standin(dev)
-        result["launch"] = bench_launch(dev)
-        result["floors"] = bench_floors(dev)
+        details["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"],
+                                    "rows": table}
+        result["decode"] = summary_decode(table)
+        for name, fn in (("quant", bench_quant), ("llama_decode", bench_llama_decode),
+                         ("prefill", bench_prefill), ("standin", bench_standin),
+                         ("launch", bench_launch), ("floors", bench_floors)):
+            details[name] = fn(dev)
+            summary = SUMMARIES[name](details[name])
+            if summary:
+                result[name] = summary
+        result["checks"] = ("every timed output checked first (poisoned outputs): sweep, Llama "
+                            "decode and prefill against float64; quantizers and every op of the "
+                            "stand-in against the reference's CPU arithmetic")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
-        result["cpu_reference_path"] = cpu_reference_path()
+        ref_path = cpu_reference_path()
+        details["cpu_reference_path"] = ref_path
+        result["cpu_baseline"] = {
+            "value": ref_path["gemm_int_mm"], "unit": "us per linear", "cores": ref_path["threads"],
+            "kind": "port",
+            "sample": "config 0 (M=16 K=2048 N=4096): the reference's CPU path in torch ops, "
+                      "torch._int_mm + fp32 dequant + bf16 cast (kernel.py:105-120), median of "
+                      "5 windows of ~0.4 s"}
+        result["cpu_reference_path"] = {k: v for k, v in ref_path.items()
+                                        if k not in ("sample", "unit")}
+        result["cpu_oracle"] = cpu_baseline()
+    # the per-point tables on lines of their own, then the one-line result (last line)
+    for name, obj in details.items():
+        print(json.dumps({"detail": name, "data": obj}), flush=True)
+    if args.details:
+        Path(args.details).write_text(json.dumps({**result, "details": details}, indent=1) + "\n")
     print(json.dumps(result), flush=True)
     return 0
 
 
+# ---------------------------------------------------------------- one-line summaries
+# The result line keeps only scalars in each section (the driver's record keeps a section's
+# scalar fields), the tables go on the lines before it.
+
+def summary_decode(table) -> dict:
+    """us and HBM fraction per Qwen3 shape at 1, 16 and 128 tokens (no bias), and the mean
+    HBM fraction over 1-16 tokens."""
+    out = {}
+    for label in dict.fromkeys(r[0] for r in table):
+        rows = {r[1]: r for r in table if r[0] == label and r[2] == 0}
+        short = label.replace("_proj", "")
+        for m in (1, 16, 128):
+            if m in rows:
+                out[f"{short}_m{m}_us"] = rows[m][3]
+        small = [rows[m][4] for m in rows if m <= 16]
+        if small:
+            out[f"{short}_m1_16_hbm_frac"] = round(sum(small) / len(small), 3)
+    return out
+
+
+def summary_prefill(pf) -> dict:
+    """The dominant launch's roofline fields, then the MFMA fraction of every shape and M."""
+    out = dict(pf.get("roofline", {}))
+    for label, m, us, tops, frac in pf["rows"]:
+        out[f"{label.replace('_proj', '')}_m{m}_frac"] = frac
+    return out
+
+
+def summary_quant(q) -> dict:
+    out = {}
+    for m, us_n, f_n, us_s, f_s in q["rows"]:
+        if m in (1, 4096):
+            out.update({f"add_rmsnorm_quant_m{m}_us": us_n, f"add_rmsnorm_quant_m{m}_frac": f_n,
+                        f"silu_mul_quant_m{m}_us": us_s, f"silu_mul_quant_m{m}_frac": f_s})
+    return out
+
+
+def summary_standin(st) -> dict:
+    out = {f"m{m}_us_per_layer": us for m, us, _ in st["rows"]}
+    out["ops_checked"] = st.get("ops_checked")
+    return out
+
+
+def summary_llama(ld) -> dict:
+    return {f"{label.replace('_proj', '')}_m{m}_frac": frac
+            for label, m, us, frac, _ in ld["rows"] if m in (1, 16, 64)}
+
+
+def summary_floors(fl) -> dict:
+    out = {"empty_kernel_us": min(r[2] for r in fl["empty_kernel"]["rows"])}
+    for mib, cache, us, gbs, frac, *_ in fl["read"]["rows"]:
+        out[f"read_{mib}MiB_{cache}_us"] = us
+    for name, operands, us, tops, frac in fl["mfma"]["rows"]:
+        out[f"mfma_{name.split('_')[3]}_{operands}_TOPs"] = tops
+    return out
+
+
+SUMMARIES = {"quant": summary_quant, "llama_decode": summary_llama, "prefill": summary_prefill,
+             "standin": summary_standin, "launch": lambda _: None, "floors": summary_floors}
+
+
 def bench_quant(dev) -> dict:
-    """the two fused quantizers at H=2048 / I=6144."""
+    """the two fused quantizers at H=2048 / I=6144.  Each size is checked
+    first: the C entry point writes into poisoned outputs (codes 99, NaN scales and residual),
+    which are compared with the reference's CPU arithmetic (ref_norm, ref_silu)."""
     import torch
 
+    from int8_linear import _lib
     from int8_linear import fused_quant as fq
+
+    def poisoned(shape, dtype=None):
+        if dtype == torch.int8:
+            return torch.full(shape, 99, dtype=torch.int8, device=dev)
+        return torch.full(shape, float("nan"), device=dev,
+                          dtype=torch.float32 if shape[1] == 1 else torch.bfloat16)
     rows = []
     for m in QUANT_M:
         g = torch.Generator().manual_seed(m)
@@ -487,9 +751,24 @@ def bench_quant(dev) -> dict:
         xs = [torch.randn((m, 2048), generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
         rs = [torch.randn((m, 2048), generator=g).to(torch.bfloat16).to(dev) for _ in range(copies)]
         w = (1 + 0.1 * torch.randn(2048, generator=g)).to(torch.bfloat16).to(dev)
+        # checked first: outputs poisoned, then against the reference's CPU arithmetic
+        q, s, rout = poisoned((m, 2048), torch.int8), poisoned((m, 1)), poisoned((m, 2048))
+        _lib.check(_lib.lib().i8l_add_rmsnorm_quant(
+            xs[0].data_ptr(), rs[0].data_ptr(), w.data_ptr(), 1e-6, q.data_ptr(), s.data_ptr(),
+            rout.data_ptr(), m, 2048, _lib.BF16, _lib.BF16, 1, _lib.stream_of(q)), RuntimeError)
+        q0, s0, r0 = ref_norm(xs[0].cpu(), rs[0].cpu(), w.cpu(), 1e-6)
+        check_quant(q, s, q0, s0, f"add_rmsnorm_quant M={m}")
+        if not torch.equal(rout.cpu(), r0):
+            raise SystemExit(f"FAIL add_rmsnorm_quant M={m}: residual_out differs")
         us_n = graph_time_us(lambda i: fq.add_rmsnorm_quant(xs[i % 2], rs[i % copies], w, 1e-6), 2 * copies, 3)
         copies_s = min(64, max(2, -(-ROTATE_BYTES // (m * 12288 * 2 + 1))))
         gus = [torch.randn((m, 12288), generator=g).to(torch.bfloat16).to(dev) for _ in range(copies_s)]
+        q, s = poisoned((m, 6144), torch.int8), poisoned((m, 1))
+        _lib.check(_lib.lib().i8l_silu_mul_quant(gus[0].data_ptr(), q.data_ptr(), s.data_ptr(), m,
+                                                 6144, _lib.BF16, 1, 1, _lib.stream_of(q)),
+                   RuntimeError)
+        q0, s0 = ref_silu(gus[0].cpu(), True)
+        check_quant(q, s, q0, s0, f"silu_mul_quant M={m}")
         us_s = graph_time_us(lambda i: fq.silu_mul_quant(gus[i % copies_s], True, True), 2 * copies_s, 3)
         rows.append([m, round(us_n, 2), round(norm_bytes(m, 2048) / (us_n * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
                      round(us_s, 2), round(silu_bytes(m, 6144) / (us_s * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)])
@@ -507,15 +786,23 @@ def bench_standin(dev) -> dict:
     base = standin.DecoderStandIn(1, generator_device="cuda")   # 1.41 GB of layer weights
     wbytes = base.weight_bytes() / len(base.layers)
     rows = []
+    checked = 0
     for m in STANDIN_M + [STANDIN_PREFILL_M]:
         st = base.with_batch(m, seed=m)
-        us = standin.per_layer_us(st, windows=5)
+        # every token row up to 128 tokens, 16 spread rows of the 4096-token step
+        rows_m = slice(None) if m <= 128 else torch.linspace(0, m - 1, 16).long()
+
+        def check(h, st=st, rows_m=rows_m):
+            nonlocal checked
+            checked += check_standin(st, rows_m, h)
+
+        us = standin.per_layer_us(st, windows=5, check=check)
         rows.append([m, round(us, 2), round(wbytes / (us * 1e-6) / 1e9, 1)])
-        log(f"standin M={m}: {us:.2f} us per layer")
+        log(f"standin M={m}: {us:.2f} us per layer (checked)")
         del st
     del base
     torch.cuda.empty_cache()
-    return {"cols": ["M", "us_per_layer", "weight_GBps"], "rows": rows,
+    return {"cols": ["M", "us_per_layer", "weight_GBps"], "rows": rows, "ops_checked": checked,
             "layers": standin.LAYERS, "weight_bytes_per_layer": int(wbytes),
             "step": "add_rmsnorm_quant > qkv > quant(q cols) > o > add_rmsnorm_quant > gate_up "
                     "> silu_mul_quant > down, one HIP graph per 28-layer step"}
@@ -544,10 +831,11 @@ def bench_llama_decode(dev) -> dict:
         for m in LLAMA_DECODE_M:
             a = operands(m, k, 64, seed_of(m, k, n), device=dev)
             a_q, a_s = a["a_q"], a["a_s"]
-            out = w8a8_mm(a_q, ws[0].t(), a_s, w_s, torch.bfloat16)
-            term = (a_q.double() @ ws[0].double().t()) * a_s.double() * w_s.double().t()
-            err = ((out.double() - term).abs() / term.abs().clamp_min(1e-6)).max().item()
-            if not err <= 1e-2:
+            dd = {"a_q": a_q, "w_q": ws[0], "a_s": a_s, "w_s": w_s, "bias": None}
+            out = checked_mm(dd)
+            err = check_linear(out, dd)
+            if not err <= 1e-2 or not torch.equal(
+                    w8a8_mm(a_q, ws[0].t(), a_s, w_s, torch.bfloat16), out):
                 raise SystemExit(f"FAIL llama decode {label} M={m}: rel err {err}")
             us = graph_time_us(lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s,
                                                  torch.bfloat16), 2 * copies, 3)
@@ -721,10 +1009,15 @@ def bench_prefill(dev, ms=None) -> dict:
             x = torch.randn((m, k), generator=g).to(torch.bfloat16)
             a_q, a_s = quant_rows(x)
             a_q, a_s = a_q.to(dev), a_s.to(dev)
-            out = w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16)
-            term = (a_q[:64].double() @ w_q.double().t()) * a_s[:64].double() * w_s.double().t()
-            err = ((out[:64].double() - term).abs() / term.abs().clamp_min(1e-6)).max().item()
-            if not err <= 1e-2:
+            out = checked_mm({"a_q": a_q, "w_q": w_q, "a_s": a_s, "w_s": w_s, "bias": None})
+            # float64 on 64 rows spread over M (several in every 256-row tile block);
+            # every element must have been written (no NaN left)
+            rows_m = torch.linspace(0, m - 1, 64).long().to(dev)
+            term = (a_q[rows_m].double() @ w_q.double().t()) * a_s[rows_m].double() * \
+                w_s.double().t()
+            err = ((out[rows_m].double() - term).abs() / term.abs().clamp_min(1e-6)).max().item()
+            if not err <= 1e-2 or bool(out.isnan().any()) or not torch.equal(
+                    w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16), out):
                 raise SystemExit(f"FAIL prefill {label} M={m}: rel err {err}")
             us = graph_time_us(lambda i: w8a8_mm(a_q, w_q.t(), a_s, w_s, torch.bfloat16), 10, 3)
             ops = 2 * m * n * k
@@ -752,6 +1045,37 @@ def bench_prefill(dev, ms=None) -> dict:
 
 
 PROBES_LIB = ROOT / "int8-linear_amd" / "probes" / "libi8l_floors.so"
+
+
+def run_linear(dev, kn: str, m: int, config: str | None, reps: int = 3) -> dict:
+    """One W8A8 linear launched repeatedly, for a profiler to watch (rocprofv3 kernel trace or
+    counters): random int8 operands of the shape, fp32 per-token and per-channel scales, bf16
+    out, the given config (bm,bn,bk,warps,stages,group_m) or the library's choice.  The
+    weights rotate through copies filling >= 768 MiB, so every launch reads them from HBM;
+    the first output is checked against float64 before the profiled launches."""
+    import torch
+
+    from int8_linear.kernel import Config, choose_config, w8a8_mm
+    k, n = map(int, kn.lower().split("x"))
+    cfg = Config(*map(int, config.split(","))) if config else choose_config(m, n, k)
+    g = torch.Generator().manual_seed(m * 7919 + k * 31 + n)
+    copies = max(2, -(-ROTATE_BYTES // (k * n)))
+    ws = [torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+          for _ in range(copies)]
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(dev)
+    sa = (torch.rand((m, 1), generator=g) * 1e-2).to(dev)
+    sb = (torch.rand((n, 1), generator=g) * 1e-2).to(dev)
+    d = {"a_q": a, "w_q": ws[0], "a_s": sa, "w_s": sb, "bias": None}
+    err = check_linear(checked_mm(d, cfg), d)
+    if not err <= 1e-2:
+        raise SystemExit(f"FAIL linear {kn} M={m} {cfg.name}: rel err {err}")
+    for _ in range(reps):
+        for w in ws:
+            w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=cfg)
+    torch.cuda.synchronize()
+    log(f"ran {reps * copies} launches: M={m} K={k} N={n} {cfg.name}")
+    return {"kn": kn, "m": m, "config": cfg.name, "launches": reps * copies,
+            "kernel": schedule_of(cfg, k)}
 
 
 def bench_floors(dev) -> dict:

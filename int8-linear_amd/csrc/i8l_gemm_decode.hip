@@ -745,8 +745,9 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * 16;
-  // valid rows of the block; the host picks P = ceil(mb / RPP), so every pass is needed and
-  // the code has no skipped (taken-branch) passes
+  // valid rows of the block; the host picks P as ceil(mb / RPP) rounded up to a power of two,
+  // so the last pass can find no valid row (e.g. 3 rows at RPP 1 run P = 4): its loads and
+  // stores are then skipped by the per-row test
   const int mb = (int)min((int64_t)16, (int64_t)e.M - m0);
   const int64_t kw = (int64_t)wave * S;
   int8_t* wbuf = lds + (size_t)wave * SB;

@@ -11,8 +11,9 @@ namespace i8l {
 // the values are computed in the fragment layout (scales and bias fetched with vector loads),
 // written to LDS as a row-major tile with 16 bytes of padding per row (so the 32 rows one
 // store instruction touches spread over the banks), and copied out with 16-byte stores,
-// 64 lanes covering consecutive columns of consecutive rows.  int32 and fp32 outputs are
-// stored straight from the fragments.  `lds` must hold BM * (2*BN + 16) bytes and every wave
+// 64 lanes covering consecutive columns of consecutive rows.  int32 and fp32 outputs take the
+// same staging half of the tile's rows at a time (BM/2 rows of 4*BN bytes fit the area).  The
+// copies out are non-temporal stores.  `lds` must hold BM * (2*BN + 16) bytes and every wave
 // must be done with its previous LDS contents.
 template <int BM, int BN, int WM, int WN>
 constexpr int tile_epilogue_lds_bytes() { return BM * (2 * BN + 16); }

@@ -247,3 +247,44 @@ def w8a8_mm(
         _cconfig(cfg), _lib.stream_of(a_q))
     _lib.check(status, NotSupported)
     return out
+
+
+def w8a8_mm_noalloc(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
+                    scale_b: torch.Tensor, out: torch.Tensor, bias: torch.Tensor | None = None,
+                    *, config: Config | None = None) -> torch.Tensor:
+    """w8a8_mm into the caller's `out` ([M, N] bf16/fp16/fp32, or int32 for the raw product),
+    allocating no device memory: the C entry i8l_w8a8_mm_noalloc, for callers that cannot
+    allocate (code under HIP graph capture, serving loops that forbid it).  It has no
+    counterpart in the reference.
+
+    A split of K (stages 5) keeps its int32 partial planes in the library's own 16 MiB device
+    array of the GPU, which every call of this entry on that GPU shares.  Calls that can
+    overlap in time on one GPU (launched on two streams with no ordering between them) race
+    on it and give wrong results: order them (one stream, or events).  Configurations whose
+    planes exceed 16 MiB raise NotSupported (use w8a8_mm).  Scales and bias are taken as they
+    are: contiguous float32 scales and a contiguous bias, or ValueError (no copies are made).
+    """
+    if a_q.dtype != torch.int8 or b_q.dtype != torch.int8:
+        raise NotSupported(f"int8 operands only, got {a_q.dtype} and {b_q.dtype}")
+    if a_q.dim() != 2 or b_q.dim() != 2 or a_q.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(a_q.shape)} by {tuple(b_q.shape)}")
+    m, k = a_q.shape
+    n = b_q.shape[1]
+    if tuple(out.shape) != (m, n) or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major [{m}, {n}] tensor")
+    same_device(a_q.device, b_q=b_q, scale_a=scale_a, scale_b=scale_b, bias=bias, out=out)
+    for name, t in (("scale_a", scale_a), ("scale_b", scale_b), ("bias", bias)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous (this entry makes no copies)")
+    if scale_a.dtype != torch.float32 or scale_b.dtype != torch.float32:
+        raise NotSupported(f"float32 scales only, got {scale_a.dtype} and {scale_b.dtype}")
+    out_code = _lib.DTYPE_CODE.get(out.dtype)
+    bias_code = _lib.DTYPE_CODE.get(bias.dtype) if bias is not None else _lib.DTYPE_NONE
+    status = _lib.lib().i8l_w8a8_mm_noalloc(
+        a_q.data_ptr(), a_q.stride(0), a_q.stride(1), b_q.data_ptr(), b_q.stride(0),
+        b_q.stride(1), scale_a.data_ptr(), scale_a.numel(), scale_b.data_ptr(), scale_b.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
+        out.stride(0), out_code if out_code is not None else -1, m, n, k,
+        _cconfig(config) if config is not None else None, _lib.stream_of(a_q))
+    _lib.check(status, NotSupported)
+    return out

@@ -128,9 +128,11 @@ class DecoderStandIn:
         return (h, res) if with_residual else h
 
 
-def per_layer_us(stack: DecoderStandIn, windows: int = 5, min_window_ms: float = 20.0) -> float:
+def per_layer_us(stack: DecoderStandIn, windows: int = 5, min_window_ms: float = 20.0,
+                 check=None) -> float:
     """Median microseconds per decoder layer, with the whole step captured as one HIP graph
-    and replayed (the reference's discipline, bench/situ_tune.py:127-154)."""
+    and replayed (the reference's discipline, bench/situ_tune.py:127-154).  `check`, if
+    given, is called with the step's output after the graph's first replay, before timing."""
     import statistics
 
     side = torch.cuda.Stream()
@@ -140,9 +142,12 @@ def per_layer_us(stack: DecoderStandIn, windows: int = 5, min_window_ms: float =
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        stack.forward()
+        h = stack.forward()
+    h.fill_(float("nan"))   # eager, outside the graph: the replay must write every element
     graph.replay()
     torch.cuda.synchronize()
+    if check is not None:
+        check(h)
 
     def window(reps: int) -> float:
         start = torch.cuda.Event(enable_timing=True)

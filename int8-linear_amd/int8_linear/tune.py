@@ -6,8 +6,11 @@ reference's sweep and merge are bench/bench_linear.py:213-227, 385-389).
     python -m int8_linear.tune --shapes qwen3-1.7b-vllm --m 1,2,4,8,16,17,32,64,128
     python -m int8_linear.tune --shapes llama-3-8b --m 512,1024,2048,4096 --merge
     python -m int8_linear.tune --shapes qwen3-1.7b-vllm --m capture --merge
+    python -m int8_linear.tune --ring-costs [--kn 8192x8192,...] [--m 48,96,...]
 
-`--m capture` is vLLM's CUDA-graph batch sizes (1, 2, 4, 8 to 248 by 8, 256 to 512 by 16)
+`--ring-costs` times the overlapped-ring tiles the library default chooses among (their
+per-wave costs are the constants of that rule) and checks the default's pick against the
+fastest of them.  `--m capture` is vLLM's CUDA-graph batch sizes (1, 2, 4, 8 to 248 by 8, 256 to 512 by 16)
 plus three prefill sizes, the M values a served decode step is padded to (the reference's
 tools/run_e2e_vm.sh:60-67).
 
@@ -232,6 +235,11 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = 
         finals = {c: [us] for us, c in timed[:FINALISTS]}
         cur = tuned_config(m, n, k)
         if cur is not None and cur not in finals and supported(m, n, k, cur):
+            # the stored entry is kept or re-recorded only if its product is checked too
+            got = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=cur)
+            if not torch.equal(got, ref):
+                raise RuntimeError(f"stored config {cur.name} gives a different product at "
+                                   f"M={m} K={k} N={n}")
             finals[cur] = [next((us for us, c in timed if c == cur), None) or time_cold_us(
                 lambda i: w8a8_mm(a_q, ws[i % copies].t(), a_s, w_s, torch.bfloat16,
                                   config=cur), copies)]
@@ -266,9 +274,87 @@ def merge(table: dict, device_key: str, path=TUNED_PATH) -> None:
     path.write_text(json.dumps(tables, indent=1, sort_keys=True) + "\n")
 
 
+# (bm, bn, bk, warps, stages, group_m) of the overlapped-ring tiles i8l_default_config
+# chooses among above the decode rules (csrc/i8l_gemm.hip)
+RING = [(64, 64, 128, 4, 12, 8), (128, 64, 128, 4, 12, 8), (64, 128, 128, 4, 12, 8),
+        (128, 128, 128, 4, 12, 8), (64, 256, 128, 8, 11, 8), (256, 128, 128, 8, 11, 8),
+        (128, 256, 128, 8, 11, 8), (256, 192, 128, 8, 10, 4), (256, 256, 128, 8, 10, 4)]
+RING_SHAPES = ("8192x10240,8192x8192,8192x57344,28672x8192,5120x5120,5120x27648,27648x5120,"
+               "5120x7168,4096x6144,2048x12288,4096x28672,14336x4096,2048x2048,6144x2048,"
+               "4096x4096")
+RING_MS = "48,96,160,200,272,400,512,768,1024,1536,2048,4096"
+
+
+def ring_costs(shapes: str = RING_SHAPES, ms: str = RING_MS, log=print) -> dict:
+    """Time the overlapped-ring tiles the library default chooses among, and check the default.
+
+    Every tile of RING is timed per (K x N, M) as a candidate is (time_cold_us).  Logged: one
+    line a case with the fastest tile and the default's time against it; then each tile's
+    time for one wave of workgroups (one a CU) per K byte, the median over the cases (the
+    per-tile constants of the default rule, relative to the 64x64 tile); then the default's
+    geometric-mean and worst ratio to the fastest tile over the cases it takes from RING.
+    """
+    import math
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    log(f"{torch.cuda.get_device_name(dev)}: {cus} CUs")
+    cases = []
+    for spec in shapes.split(","):
+        k, n = map(int, spec.lower().split("x"))
+        g = torch.Generator().manual_seed(k * 31 + n)
+        copies = max(2, -(-(768 << 20) // (k * n)))
+        ws = [torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+              for _ in range(copies)]
+        for m in map(int, ms.split(",")):
+            a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(dev)
+            sa = torch.rand((m, 1), generator=g).to(dev)
+            sb = torch.rand((n, 1), generator=g).to(dev)
+            t = {}
+            for c in RING:
+                cfg = Config(*c)
+                if supported(m, n, k, cfg):
+                    t[c] = time_cold_us(lambda i, cfg=cfg: w8a8_mm(
+                        a, ws[i % copies].t(), sa, sb, torch.bfloat16, None, config=cfg), copies)
+            d = default_config(m, n, k)
+            dc = (d.bm, d.bn, d.bk, d.warps, d.stages, d.group_m)
+            best = min(t, key=t.get)
+            rel = f"{t[dc] / t[best]:.3f}" if dc in t else "not a ring tile"
+            log(f"K={k} N={n} M={m}: fastest {Config(*best).name} {t[best]:.2f} us; "
+                f"default {Config(*dc).name} {rel}")
+            cases.append((k, n, m, t, dc))
+        del ws
+        torch.cuda.empty_cache()
+    per = {c: [] for c in RING}
+    for k, n, m, t, _ in cases:
+        for c, us in t.items():
+            waves = math.ceil(math.ceil(m / c[0]) * (n // c[1]) / cus)
+            per[c].append(us * 1e3 / (k * waves))
+    base = statistics.median(per[RING[0]]) if per[RING[0]] else float("nan")
+    log("one wave's time per K byte (median over the cases), relative to 64x64:")
+    costs = {}
+    for c in RING:
+        if per[c]:
+            med = statistics.median(per[c])
+            costs[Config(*c).name] = round(med, 4)
+            log(f"  {c[0]}x{c[1]}: {med:.3f} ns ({100 * med / base:.0f})")
+    out = {"wave_ns_per_k_byte": costs}
+    ratios = [t[dc] / min(t.values()) for _, _, _, t, dc in cases if dc in t]
+    if ratios:
+        out["default_vs_fastest_geomean"] = round(
+            math.exp(sum(map(math.log, ratios)) / len(ratios)), 4)
+        out["default_vs_fastest_worst"] = round(max(ratios), 4)
+        log(f"default against the fastest ring tile over {len(ratios)} cases: geometric mean "
+            f"{out['default_vs_fastest_geomean']:.3f}, worst {out['default_vs_fastest_worst']:.3f}")
+    return out
+
+
 def main() -> int:
     from int8_linear.shapes import SHAPES
     ap = argparse.ArgumentParser()
+    ap.add_argument("--ring-costs", action="store_true",
+                    help="time the default rule's overlapped-ring tiles (--kn: K x N shapes, "
+                         "--m: token counts; defaults: 15 shapes at 48-4096 tokens)")
     ap.add_argument("--shapes", default="qwen3-1.7b-vllm")
     ap.add_argument("--m", default="1,2,4,8,16,17,32,64,128",
                     help="comma-separated M values, or capture (vLLM graph batch sizes)")
@@ -283,6 +369,12 @@ def main() -> int:
                          "(e.g. 0.02)")
     ap.add_argument("--out", default=None, help="also write the result to this JSON file")
     args = ap.parse_args()
+    if args.ring_costs:
+        res = ring_costs(args.kn or RING_SHAPES,
+                         RING_MS if args.m == ap.get_default("m") else args.m,
+                         log=lambda *a: print(*a, file=sys.stderr, flush=True))
+        print(json.dumps(res))
+        return 0
     dev = torch.device("cuda:0")
     arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
     ms = parse_ms(args.m)

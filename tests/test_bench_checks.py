@@ -1,0 +1,102 @@
+"""The bench's own output checks, on the CPU: the reference's CPU arithmetic that bench.py
+compares the timed quantizers and stand-in ops with (ref_mm, ref_norm, ref_silu, ref_quant,
+check_quant) must accept the oracle's outputs, which the GPU matches bit for bit, and must
+reject a planted mistake; and the one-line result keeps only scalars in each section (the
+driver's record keeps a section's scalar fields).
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from helpers import from_bits
+from oracle import oracle as o
+
+
+def _bf16(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_ref_mm_is_the_oracle_bit_for_bit():
+    """The reference's CPU path of a linear (torch._int_mm, fp32 dequant, one cast) is the
+    oracle's epilogue order, so the bench's GEMM check is bit equality."""
+    g = torch.Generator().manual_seed(3)
+    for m, k, n in ((1, 2048, 4096), (8, 6144, 2048), (5, 256, 96)):
+        q = torch.randint(-128, 128, (m, k), dtype=torch.int8, generator=g)
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
+        s = torch.rand((m, 1), generator=g) * 1e-2 + 1e-3
+        ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-4
+        got = bench.ref_mm(q, s, w, ws)
+        ref = o.w8a8_mm(q.numpy(), w.numpy(), s.numpy(), ws.numpy(), out_dt=o.BF16)
+        assert np.array_equal(_bits(got), ref)
+
+
+def test_quantizer_checks_accept_the_oracle():
+    x, r = _bf16((64, 2048), 1), _bf16((64, 2048), 2)
+    gamma = (1 + 0.1 * torch.randn(2048, generator=torch.Generator().manual_seed(3))).to(
+        torch.bfloat16)
+    q, s, rout = o.add_rmsnorm_quant(_bits(x), _bits(r), _bits(gamma), 1e-6)
+    q0, s0, r0 = bench.ref_norm(x, r, gamma, 1e-6)
+    bench.check_quant(torch.from_numpy(q), torch.from_numpy(s), q0, s0, "norm")
+    assert torch.equal(from_bits(rout, device="cpu"), r0)
+    gu = _bf16((64, 12288), 4)
+    for round_silu in (False, True):
+        q, s = o.silu_mul_quant(_bits(gu), round_silu=round_silu)
+        q0, s0 = bench.ref_silu(gu, round_silu)
+        bench.check_quant(torch.from_numpy(q), torch.from_numpy(s), q0, s0, "silu")
+    y = _bf16((16, 2048), 5).float()
+    q, s = o.quant_per_token(_bits(y.to(torch.bfloat16)))
+    q0, s0 = bench.ref_quant(y.to(torch.bfloat16).float())
+    bench.check_quant(torch.from_numpy(q), torch.from_numpy(s), q0, s0, "quant")
+
+
+def test_quantizer_check_rejects_planted_mistakes():
+    gu = _bf16((16, 12288), 6)
+    q, s = (torch.from_numpy(a) for a in o.silu_mul_quant(_bits(gu), round_silu=True))
+    q0, s0 = bench.ref_silu(gu, True)
+    bench.check_quant(q, s, q0, s0, "silu")
+    two = q.clone()
+    two[3, 7] = (two[3, 7].int() + 2).clamp(-128, 127).to(torch.int8)
+    with pytest.raises(SystemExit):
+        bench.check_quant(two, s, q0, s0, "code off by two")
+    many = q.clone()
+    many[:, :100] = (many[:, :100].int() + 1).clamp(-128, 126).to(torch.int8)
+    with pytest.raises(SystemExit):
+        bench.check_quant(many, s, q0, s0, "1600 codes off by one")
+    with pytest.raises(SystemExit):
+        bench.check_quant(q, s * (1 + 1e-4), q0, s0, "scales off")
+    with pytest.raises(SystemExit):
+        bench.check_quant(q, torch.full_like(s, float("nan")), q0, s0, "scales never written")
+
+
+def test_result_sections_are_scalars():
+    """Each summary section of the one-line result holds scalars only, from tables shaped
+    as the bench's legs return them."""
+    decode = [["qkv_proj", m, b, 3.5, 0.3] for m in bench.DECODE_M for b in (0, 1)]
+    prefill = {"rows": [["qkv_proj", m, 100.0, 2000.0, 0.4] for m in bench.PREFILL_M],
+               "roofline": {"bound": "mfma", "achieved": 2000.0, "peak": 5000.0,
+                            "unit": "TOP/s", "frac": 0.4, "traffic": None, "kernel": "k"}}
+    quant = {"rows": [[m, 2.0, 0.1, 3.0, 0.2] for m in bench.QUANT_M]}
+    standin = {"rows": [[m, 25.0, 2000.0] for m in bench.STANDIN_M + [4096]], "ops_checked": 9}
+    llama = {"rows": [["gate_up_proj", m, 19.0, 0.76, "k"] for m in bench.LLAMA_DECODE_M]}
+    floors = {"empty_kernel": {"rows": [[1, 64, 1.6]]},
+              "read": {"rows": [[8, "cold", 2.9, 2900.0, 0.36, 4, {}]]},
+              "mfma": {"rows": [["v_mfma_i32_32x32x32_i8", "random", 1.0, 3500.0, 0.7]]}}
+    for fn, table in ((bench.summary_decode, decode), (bench.summary_prefill, prefill),
+                      (bench.summary_quant, quant), (bench.summary_standin, standin),
+                      (bench.summary_llama, llama), (bench.summary_floors, floors)):
+        out = fn(table)
+        assert out and all(isinstance(v, (int, float, str, type(None))) for v in out.values()), fn
+        json.dumps(out)
+    assert bench.summary_prefill(prefill)["qkv_m4096_frac"] == 0.4
+    assert bench.summary_standin(standin)["m1_us_per_layer"] == 25.0

@@ -247,7 +247,7 @@ WLDS = [(mt, nc, ks) for mt, nc, ks in
 
 @pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
 @pytest.mark.parametrize("steps", [1, 2, 3, 4])
-@pytest.mark.parametrize("waves", [4, 8, 16])
+@pytest.mark.parametrize("waves", [4, 8, 12, 16])
 def test_weights_through_lds_schedule(tile, steps, waves):
     mt, nc, ks = tile
     k, n = 64 * ks * waves * steps, 512

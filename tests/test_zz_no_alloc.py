@@ -82,3 +82,79 @@ def test_noalloc_declines_beyond_its_scratch_and_runs_unsplit_configs():
         assert _call(L.i8l_w8a8_mm_noalloc, a, w, one, one, None, out, _lib.I32, c) == _lib.OK
         torch.cuda.synchronize()
         assert np.array_equal(np_(out), o.gemm_i32(np_(a), np_(w)))
+
+
+def test_python_wrapper_matches_w8a8_mm():
+    """int8_linear.kernel.w8a8_mm_noalloc (into the caller's out) gives w8a8_mm's bits, with
+    a split of K and without, and refuses operands it would have to copy."""
+    k, n = 6144, 2048
+    w = ints((n, k), 71)
+    g = torch.Generator().manual_seed(72)
+    sb = (torch.rand((n,), generator=g) * 1e-3 + 1e-4).cuda()
+    for m, cfg in ((64, Config(64, 64, 128, 4, 5, 4)), (9, None)):
+        say(f"noalloc wrapper m={m} {cfg.name if cfg else 'default'}")
+        a = ints((m, k), 73 + m)
+        sa = (torch.rand((m,), generator=g) * 1e-2 + 1e-3).cuda()
+        out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        got = kernel.w8a8_mm_noalloc(a, w.t(), sa, sb, out, config=cfg)
+        assert got is out
+        ref = kernel.w8a8_mm(a, w.t(), sa, sb, torch.bfloat16, config=cfg)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    with pytest.raises(ValueError):
+        kernel.w8a8_mm_noalloc(a, w.t(), torch.rand((m, 2), device="cuda")[:, 0], sb, out)
+
+
+# A fresh process whose first use of the library is an allocation-free split-of-K call under
+# HIP graph capture (so the device's scratch address is looked up inside the capture), then
+# replays with new activations checked against the workspace entry.
+_CAPTURE = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1], sys.argv[1] + "/int8-linear_amd"]
+import torch
+from int8_linear import Config, _lib, kernel
+L = _lib.lib()
+dev = torch.device("cuda:0")
+m, k, n = 96, 14336, 4096
+cfg = Config(64, 64, 128, 4, 5, 4)
+c = kernel._cconfig(cfg)
+g = torch.Generator().manual_seed(5)
+w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).to(dev)
+a = torch.empty((m, k), dtype=torch.int8, device=dev)
+sa = (torch.rand((m,), generator=g) * 1e-2 + 1e-3).to(dev)
+sb = (torch.rand((n,), generator=g) * 1e-3 + 1e-4).to(dev)
+out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+def call(entry, o, *ws):
+    return entry(a.data_ptr(), k, 1, w.data_ptr(), 1, k, sa.data_ptr(), m, sb.data_ptr(), n,
+                 None, _lib.DTYPE_NONE, o.data_ptr(), n, _lib.BF16, m, n, k, *ws,
+                 ctypes.byref(c), torch.cuda.current_stream().cuda_stream)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    st = call(L.i8l_w8a8_mm_noalloc, out)
+assert st == _lib.OK, _lib.last_error()
+print("captured", flush=True)
+need = L.i8l_w8a8_mm_workspace_bytes(m, n, k, ctypes.byref(c))
+ws = torch.empty(need, dtype=torch.uint8, device=dev)
+ref = torch.empty_like(out)
+for r in range(4):
+    a.copy_(torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).to(dev))
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert call(L.i8l_w8a8_mm_ws, ref, ws.data_ptr(), need) == _lib.OK, _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {r} differs"
+    print("replay", r, "equal", flush=True)
+print("ok", flush=True)
+"""
+
+
+def test_first_call_inside_a_graph_capture():
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    say("noalloc: first call of a fresh process under graph capture, 4 replays")
+    r = subprocess.run([sys.executable, "-c", _CAPTURE, root], capture_output=True, text=True,
+                       timeout=150)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), (r.stdout[-2000:],
+                                                                  r.stderr[-2000:])
