@@ -782,6 +782,7 @@ def bench_standin(dev) -> dict:
     replay, microseconds per decoder layer, at decode M and one 4096-token prefill."""
     import torch
 
+    from int8_linear import fused_quant as fq
     from int8_linear import standin
     base = standin.DecoderStandIn(1, generator_device="cuda")   # 1.41 GB of layer weights
     wbytes = base.weight_bytes() / len(base.layers)
@@ -805,7 +806,10 @@ def bench_standin(dev) -> dict:
     return {"cols": ["M", "us_per_layer", "weight_GBps"], "rows": rows, "ops_checked": checked,
             "layers": standin.LAYERS, "weight_bytes_per_layer": int(wbytes),
             "step": "add_rmsnorm_quant > qkv > quant(q cols) > o > add_rmsnorm_quant > gate_up "
-                    "> silu_mul_quant > down, one HIP graph per 28-layer step"}
+                    "> silu_mul_quant > down, one HIP graph per 28-layer step; folded into one "
+                    "launch each where few tokens make it pay: norm+qkv and norm+gate_up up to "
+                    f"{fq.NORM_MM_FOLD_M} tokens, quant+o up to {fq.QUANT_MM_MAX_M}, "
+                    f"silu_mul_quant+down up to {fq.SILU_MM_MAX_M}"}
 
 
 LLAMA_DECODE_M = [1, 4, 16, 64, 128]

@@ -251,6 +251,38 @@ int i8l_silu_mul_quant_mm(const void* gate_up, int64_t ldgu, int32_t act_dtype,
  * host-only. */
 int i8l_silu_mul_quant_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
 
+/*
+ * add + RMSNorm + per-token int8 quantize and the W8A8 matmul in one launch, for few tokens:
+ *   (q, s, residual_out) = i8l_add_rmsnorm_quant(x, residual, weight, eps)
+ *   out = i8l_w8a8_mm(q, b, scale_a = s, scale_b, bias)
+ * bit for bit (same precise_div).  x, residual and residual_out are [M,K] contiguous of
+ * act_dtype (bf16/f16), weight [K] of act_dtype; residual and residual_out are both NULL
+ * (plain RMSNorm, rmsnorm_quant) or both given.  residual_out is written once (by one
+ * workgroup).  Every workgroup normalizes the token rows itself, so M is at most 8 (larger
+ * M returns I8L_UNSUPPORTED; use the two calls).  scale_a_out, if not NULL, receives the M
+ * per-token scales.  b must be K-contiguous (stride_bk == 1) and 16-byte aligned, every
+ * activation pointer and out 16-byte aligned with 16-byte row pitch.  cfg is a persistent
+ * single-step tile of this form (bm 16, bn 8 or 16, bk 256 or 512, 4 or 8 waves, stages 4,
+ * K == warps * bk a power of two, group_m workgroups a compute unit) or NULL for the
+ * library's choice.
+ *
+ * Replaces the pair the reference's stand-in issues before its qkv and gate_up projections,
+ * add_rmsnorm_quant then _w8a8_mm (bench/fuse_quant.py:226-240 of AshrithaG/int8-linear;
+ * int8_linear/fused_quant.py:56-73, 95-110 and kernel.py:202-257).
+ */
+int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, const void* weight, float eps,
+                             int32_t act_dtype, int32_t precise_div, void* residual_out,
+                             const int8_t* b, int64_t stride_bk, int64_t stride_bn,
+                             const float* scale_b, int64_t scale_b_len,
+                             const void* bias, int32_t bias_dtype,
+                             void* out, int64_t stride_cm, int32_t out_dtype, float* scale_a_out,
+                             int64_t M, int64_t N, int64_t K,
+                             const i8l_config* cfg, void* stream);
+
+/* Whether i8l_add_rmsnorm_quant_mm takes (M,N,K,cfg) (cfg NULL: the library's choice);
+ * host-only. */
+int i8l_add_rmsnorm_quant_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
+
 /* Thread-local description of the last failure ("" if none). */
 const char* i8l_last_error(void);
 

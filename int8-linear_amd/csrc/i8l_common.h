@@ -144,6 +144,43 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Doubles moved across lanes as two 32-bit halves.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = dpp_i<CTRL>((int)(uint32_t)u), hi = dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+__device__ __forceinline__ double swz16_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)u, kSwizzleXor16);
+  const int hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), kSwizzleXor16);
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const int hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
+}
+
+// Sum over each aligned group of G lanes (G = 16, 32 or 64) as a perfect binary tree, lane
+// i of the group being leaf i; every lane returns its group's sum.  Pairs, quads, then (each
+// quad being uniform) a mirror within 8 lanes and within 16 pairs the blocks below them, a
+// swizzle pairs the 16-lane halves of 32, and the two 32-lane halves are read back last.
+// IEEE addition is commutative, so both partners of each step hold the same node.
+template <int G>
+__device__ __forceinline__ double group_tree_sum(double v) {
+  static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
+  v = v + dpp_d<kQuadSwap1>(v);    // pairs
+  v = v + dpp_d<kQuadSwap2>(v);    // quads
+  v = v + dpp_d<kHalfMirror>(v);   // 8 lanes
+  v = v + dpp_d<kRowMirror>(v);    // 16 lanes
+  if constexpr (G >= 32) v = v + swz16_d(v);   // 32 lanes
+  if constexpr (G == 64) v = readlane_d(v, 0) + readlane_d(v, 32);
+  return v;
+}
+
 // ---------------------------------------------------------------- errors
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* where);

@@ -228,6 +228,26 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
+// no LDS read of the DMA'd data is scheduled above the wait.  Vector memory loads (the
+// direct-to-LDS copies among them) complete in issue order, so vmcnt(N) means that all but
+// the N most recent loads have landed.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_wlds() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt lgkmcnt(0) (vector memory and EXP counters unconstrained): the wave's LDS reads
+// have returned their data.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) int8_t lds_i8_t;
+
 // ------------------------------------------------------------------ host helpers
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -272,6 +292,14 @@ bool default_dq_config(int64_t N, int64_t K, i8l_config* c);
 bool dq_silu_ok(const i8l_config& c, int64_t K);
 bool default_dq_silu_config(int64_t N, int64_t K, i8l_config* c);
 int dq_silu_max_rows();
+// add + RMSNorm + quantize folded into the persistent decode GEMM (i8l_gemm_norm.hip).
+bool nq_ok(const i8l_config& c, int64_t K);
+bool default_nq_config(int64_t M, int64_t N, int64_t K, i8l_config* c);
+int nq_max_rows();
+hipError_t launch_nq(const i8l_config& c, int act_dtype, const uint16_t* x,
+                     const uint16_t* residual, const uint16_t* gamma, float eps,
+                     uint16_t* residual_out, const int8_t* b, int64_t ldb, const Epi& e,
+                     float* sa_out, int precise, hipStream_t st);
 hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
                      const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
                      hipStream_t st);

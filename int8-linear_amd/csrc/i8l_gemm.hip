@@ -552,6 +552,111 @@ extern "C" int i8l_silu_mul_quant_mm(const void* gate_up, int64_t ldgu, int32_t 
   return hip_status(err, "i8l_silu_mul_quant_mm launch");
 }
 
+// ------------------------------------------------------------------ add + RMSNorm + quant + GEMM
+extern "C" int i8l_add_rmsnorm_quant_mm_supported(int64_t M, int64_t N, int64_t K,
+                                                  const i8l_config* cfg) {
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_nq_config(M, N, K, &c)) {
+    set_error("no built norm-quant tile takes K=%lld, N=%lld", (long long)K, (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  if (M < 0 || M > nq_max_rows() || N > INT32_MAX || K > INT32_MAX) {
+    set_error("the add+RMSNorm+quant matmul takes up to %d tokens, got %lld", nq_max_rows(),
+              (long long)M);
+    return I8L_UNSUPPORTED;
+  }
+  if (c.bn <= 0 || N % c.bn || !nq_ok(c, K)) {
+    set_error("config %dx%dx%d w%d s%d g%d is not a built norm-quant tile for N=%lld K=%lld",
+              c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, (long long)N, (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  return I8L_OK;
+}
+
+extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, const void* weight,
+                                        float eps, int32_t act_dtype, int32_t precise_div,
+                                        void* residual_out, const int8_t* b, int64_t stride_bk,
+                                        int64_t stride_bn, const float* scale_b,
+                                        int64_t scale_b_len, const void* bias,
+                                        int32_t bias_dtype, void* out, int64_t stride_cm,
+                                        int32_t out_dtype, float* scale_a_out, int64_t M,
+                                        int64_t N, int64_t K, const i8l_config* cfg,
+                                        void* stream) {
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("negative size M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    return I8L_INVALID_ARG;
+  }
+  if (act_dtype != I8L_BF16 && act_dtype != I8L_F16) {
+    set_error("activations and norm weight must be bf16 or fp16 (code %d)", act_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (out_dtype != I8L_BF16 && out_dtype != I8L_F16 && out_dtype != I8L_F32) {
+    set_error("unsupported output dtype code %d", out_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if (scale_b_len != 1 && scale_b_len != N) {
+    set_error("scale_b has %lld values for N=%lld", (long long)scale_b_len, (long long)N);
+    return I8L_INVALID_ARG;
+  }
+  if (bias_dtype != I8L_DTYPE_NONE && bias_dtype != I8L_BF16 && bias_dtype != I8L_F16 &&
+      bias_dtype != I8L_F32) {
+    set_error("unsupported bias dtype code %d", bias_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if ((bias_dtype == I8L_DTYPE_NONE) != (bias == nullptr)) {
+    set_error("bias pointer and bias dtype disagree");
+    return I8L_INVALID_ARG;
+  }
+  if ((residual == nullptr) != (residual_out == nullptr)) {
+    set_error("residual and residual_out must both be given or both be NULL");
+    return I8L_INVALID_ARG;
+  }
+  if (x == nullptr || weight == nullptr) {
+    set_error("x and the norm weight are required");
+    return I8L_INVALID_ARG;
+  }
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_nq_config(M, N, K, &c)) {
+    set_error("no built norm-quant tile takes K=%lld, N=%lld", (long long)K, (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  const int st = i8l_add_rmsnorm_quant_mm_supported(M, N, K, &c);
+  if (st != I8L_OK) return st;
+  if (M == 0 || N == 0) return I8L_OK;
+  const int osz = elt_size(out_dtype);
+  const bool layout = stride_bk == 1 && aligned16(b) && stride_bn % 16 == 0 &&
+                      stride_bn <= INT32_MAX / 32 && aligned16(x) && aligned16(weight) &&
+                      (residual == nullptr || (aligned16(residual) && aligned16(residual_out))) &&
+                      aligned16(out) && (stride_cm * osz) % 16 == 0 && stride_cm >= N &&
+                      N % 4 == 0 && (scale_b_len == 1 || aligned16(scale_b)) &&
+                      (bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
+  if (!layout) {
+    set_error("the norm-quant path needs K-contiguous 16-byte aligned operands");
+    return I8L_UNSUPPORTED;
+  }
+  Epi e;
+  e.sa = nullptr;
+  e.sb = scale_b;
+  e.bias = bias;
+  e.out = out;
+  e.ldc = stride_cm;
+  e.sa_per_row = 1;
+  e.sb_per_col = scale_b_len == N && N > 1;
+  e.bias_dtype = bias_dtype;
+  e.out_dtype = out_dtype;
+  e.M = (int)M;
+  e.N = (int)N;
+  const hipError_t err = launch_nq(c, act_dtype, (const uint16_t*)x, (const uint16_t*)residual,
+                                   (const uint16_t*)weight, eps, (uint16_t*)residual_out, b,
+                                   stride_bn, e, scale_a_out, precise_div ? 1 : 0,
+                                   (hipStream_t)stream);
+  return hip_status(err, "i8l_add_rmsnorm_quant_mm launch");
+}
+
 // ------------------------------------------------------------------ allocation-free entry
 // i8l_w8a8_mm_noalloc: i8l_w8a8_mm for callers that cannot allocate (code under HIP graph
 // capture, serving loops that forbid allocation), with the split of K's partial planes in

@@ -153,16 +153,6 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // of an [Z][M][ldc] int32 buffer (the Epi's output, raw); splitk_sum adds the planes and
 // applies the epilogue.
 
-// s_waitcnt vmcnt(N) (LGKM and EXP counters unconstrained), then a compiler fence so that
-// no LDS read of the DMA'd data is scheduled above the wait.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_wlds() {
-  static_assert(N >= 0 && N < 64, "vmcnt out of range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
-
-typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 
 // The end of the multi-step weights-through-LDS tiles: sum the W waves' partial products
 // (int32 addition is exact and order-free) through an LDS area that aliases the step ring

@@ -35,35 +35,9 @@ namespace {
 constexpr int kMaxWaves = 16;  // waves per workgroup (1024 threads)
 
 // ------------------------------------------------------------------ cross-lane moves
-// (DPP controls and dpp_i are in i8l_common.h)
-template <int CTRL>
-__device__ __forceinline__ double dpp_d(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const int lo = dpp_i<CTRL>((int)(uint32_t)u), hi = dpp_i<CTRL>((int)(uint32_t)(u >> 32));
-  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
-}
-__device__ __forceinline__ double swz16_d(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)u, kSwizzleXor16);
-  const int hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), kSwizzleXor16);
-  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
-}
-__device__ __forceinline__ double readlane_d(double v, int lane) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const int lo = __builtin_amdgcn_readlane((int)(uint32_t)u, lane);
-  const int hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
-  return __builtin_bit_cast(double, (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32));
-}
-
+// (DPP controls, dpp_i and group_tree_sum are in i8l_common.h)
 // Sum over the 64 lanes as a perfect binary tree (lane i is leaf i); every lane returns it.
-__device__ __forceinline__ double wave_tree_sum(double v) {
-  v = v + dpp_d<kQuadSwap1>(v);    // pairs
-  v = v + dpp_d<kQuadSwap2>(v);    // quads
-  v = v + dpp_d<kHalfMirror>(v);   // 8 lanes: each quad is uniform, so mirroring pairs quads
-  v = v + dpp_d<kRowMirror>(v);    // 16 lanes
-  v = v + swz16_d(v);              // 32 lanes
-  return readlane_d(v, 0) + readlane_d(v, 32);
-}
+__device__ __forceinline__ double wave_tree_sum(double v) { return group_tree_sum<64>(v); }
 
 __device__ __forceinline__ float fmax_dpp1(float v) {
   return fmaxf(v, __int_as_float(dpp_i<kQuadSwap1>(__float_as_int(v))));

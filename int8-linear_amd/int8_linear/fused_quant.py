@@ -264,6 +264,78 @@ def silu_mul_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
     return _lib.lib().i8l_silu_mul_quant_mm_supported(m, n, k, cfg) == _lib.OK
 
 
+# Largest M that add_rmsnorm_quant_mm takes (the kernel's limit): every workgroup normalizes
+# and quantizes the token rows itself, while its first weight tile is in flight.
+NORM_MM_MAX_M = 8
+# Largest M for which the decoder stand-in folds the norm into its projections.  The row work
+# every workgroup repeats is ~0.24 us of VALU a token row on each compute unit, so the fold
+# pays only for few tokens: measured on MI355X (HIP graph, cold weights, K = 2048), one launch
+# against add_rmsnorm_quant + w8a8_mm at N = 4096 is 4.41 / 4.77 / 6.02 / 8.24 us against
+# 5.92 / 6.35 / 6.42 / 6.32 us at 1 / 2 / 4 / 8 tokens, at N = 12288 6.58 / 6.68 / 8.39 /
+# 11.09 against 8.74 / 8.78 / 8.64 / 8.89 us.
+NORM_MM_FOLD_M = 4
+
+
+def add_rmsnorm_quant_mm(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
+                         eps: float, b_q: torch.Tensor, scale_b: torch.Tensor,
+                         out_dtype: torch.dtype = torch.bfloat16,
+                         bias: torch.Tensor | None = None, precise_div: bool = True, *,
+                         config=None, return_scale: bool = False):
+    """add_rmsnorm_quant(x, residual, weight, eps) followed by w8a8_mm, as one kernel, for up
+    to NORM_MM_MAX_M tokens: (out [M, N], residual_out [M, K] or None), and the per-token
+    scales [M, 1] last with return_scale.
+
+    Bit for bit the two calls (reference fused_quant.py:56-73, 95-110 then kernel.py:202-257
+    in one launch): out = w8a8_mm(q, b_q, s, scale_b, out_dtype, bias) with (q, s,
+    residual_out) = add_rmsnorm_quant(x, residual, weight, eps, precise_div).  x and residual
+    are contiguous bf16/fp16 [M, K], weight [K] of x's dtype, b_q the K-contiguous [K, N]
+    view of an [N, K] weight.  Raises NotSupported for more tokens, a K no built tile takes,
+    or layouts the fused kernel does not read (the caller then makes the two calls).
+    """
+    from int8_linear.kernel import Config, _cconfig
+    if x.dim() != 2 or b_q.dim() != 2 or x.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(x.shape)} by {tuple(b_q.shape)}")
+    act = _act_code(x, "x")
+    M, K = x.shape
+    if M > NORM_MM_MAX_M:
+        raise NotSupported(f"add_rmsnorm_quant_mm takes up to {NORM_MM_MAX_M} tokens, got {M}")
+    if weight.numel() != K:
+        raise ValueError(f"weight has {weight.numel()} values for rows of {K}")
+    if weight.dtype != x.dtype:
+        raise NotSupported("the fused kernel takes a norm weight of x's dtype")
+    if not x.is_contiguous():
+        raise NotSupported("x must be contiguous")
+    weight = weight.contiguous()
+    same_device(x.device, weight=weight, residual=residual)
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != x.dtype or not residual.is_contiguous():
+            raise NotSupported("residual must be a contiguous tensor of x's shape and dtype")
+    N, sb, bias, bias_code, out_code = _mm_operands(x, b_q, scale_b, bias, out_dtype,
+                                                    "add_rmsnorm_quant_mm")
+    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    rout = torch.empty_like(x) if residual is not None else None
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device) if return_scale else None
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    status = _lib.lib().i8l_add_rmsnorm_quant_mm(
+        x.data_ptr(), residual.data_ptr() if residual is not None else None, weight.data_ptr(),
+        float(eps), act, int(bool(precise_div)), rout.data_ptr() if rout is not None else None,
+        b_q.data_ptr(), b_q.stride(0), b_q.stride(1), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
+        out.stride(0), out_code, s.data_ptr() if s is not None else None, M, N, K, cfg,
+        _lib.stream_of(x))
+    _lib.check(status, NotSupported)
+    return (out, rout, s) if return_scale else (out, rout)
+
+
+def add_rmsnorm_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
+    """Whether add_rmsnorm_quant_mm takes M tokens of hidden size K into an [N, K] weight."""
+    from int8_linear.kernel import Config, _cconfig
+    if m > NORM_MM_MAX_M:
+        return False
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    return _lib.lib().i8l_add_rmsnorm_quant_mm_supported(m, n, k, cfg) == _lib.OK
+
+
 # Numerics the custom ops use (reference fused_quant.py:127-129 defaults);
 # vllm_fuse_patch.use_measured_numerics switches them to the served configuration.
 PRECISE_DIV = True

@@ -17,8 +17,10 @@ The reference slices the q columns with .contiguous() and then quantizes them
 each layer issues 8 kernels instead of 9, and the values are the same.  Up to
 fused_quant.QUANT_MM_MAX_M tokens, the quantizer and o_proj are one kernel
 (fused_quant.quant_mm), and for the few tokens fused_quant.silu_mul_quant_mm takes,
-SiLU-and-mul+quant and down_proj are one kernel too; each gives the same bits as the two
-kernels it replaces: 6 kernels a layer at 1 token.
+SiLU-and-mul+quant and down_proj are one kernel too, and up to
+fused_quant.NORM_MM_FOLD_M tokens each add+RMSNorm+quant is folded into the projection
+after it (fused_quant.add_rmsnorm_quant_mm); each gives the same bits as the two kernels it
+replaces: 4 kernels a layer at 1 token.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
@@ -56,8 +58,12 @@ class DecoderStandIn:
         self.m = m
         # per-linear configurations ({name: Config}); a linear not named takes choose_config
         self.configs: dict = {}
+        # the same for the norm-folded linears ({name: Config}, else the library's choice)
+        self.norm_configs: dict = {}
         # fold silu_mul_quant into down_proj where the library takes it (fused_down)
         self.use_fused_down = True
+        # fold add_rmsnorm_quant into qkv_proj and gate_up_proj where the library takes it
+        self.use_fused_norm = True
         self.x = torch.randn((m, HIDDEN), generator=g, device=generator_device).to(
             torch.bfloat16).to(dev)
         self.norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
@@ -92,6 +98,14 @@ class DecoderStandIn:
         folded into the GEMM), for few tokens; otherwise silu_mul_quant runs on its own."""
         return self.use_fused_down and fq.silu_mul_quant_mm_supported(self.m, HIDDEN, INTER)
 
+    @property
+    def fused_norm(self) -> bool:
+        """Whether qkv_proj and gate_up_proj take the hidden state unnormalized (add+RMSNorm+
+        quant folded into the GEMM), for few tokens; otherwise add_rmsnorm_quant runs alone."""
+        return self.use_fused_norm and self.m <= fq.NORM_MM_FOLD_M and all(
+            fq.add_rmsnorm_quant_mm_supported(self.m, SHAPES[name][1], HIDDEN)
+            for name in ("qkv_proj", "gate_up_proj"))
+
     def weight_bytes(self) -> int:
         return sum(w.numel() + 4 * s.numel() for layer in self.layers for w, s in layer.values())
 
@@ -99,25 +113,39 @@ class DecoderStandIn:
         w, ws = layer[name]
         return w8a8_mm(q, w.t(), s, ws, torch.bfloat16, config=self.configs.get(name))
 
+    def norm_mm(self, layer, name: str, x: torch.Tensor, res: torch.Tensor | None):
+        """add_rmsnorm_quant then the linear, as one kernel: (output, residual_out)."""
+        w, ws = layer[name]
+        return fq.add_rmsnorm_quant_mm(x, res, self.norm, EPS, w.t(), ws, torch.bfloat16, None,
+                                       fq.PRECISE_DIV, config=self.norm_configs.get(name))
+
     def forward(self, with_residual: bool = False):
         """One step through every layer; returns the last down_proj output [m, HIDDEN] (and
         the residual stream entering the last layer's MLP norm, with_residual=True)."""
-        fused_o, fused_down = self.fused_o, self.fused_down
+        fused_o, fused_down, fused_norm = self.fused_o, self.fused_down, self.fused_norm
         res = self.x
-        q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
+        if not fused_norm:
+            q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
         h = None
         for i, layer in enumerate(self.layers):
-            if i:
-                q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
-            a = self.mm(layer, "qkv_proj", q, s)
+            if fused_norm:
+                a, rout = self.norm_mm(layer, "qkv_proj", h if i else self.x, res if i else None)
+                res = rout if i else res
+            else:
+                if i:
+                    q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
+                a = self.mm(layer, "qkv_proj", q, s)
             if fused_o:
                 w, ws = layer["o_proj"]
                 h = fq.quant_mm(a[:, :Q_COLS], w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV)
             else:
                 q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
                 h = self.mm(layer, "o_proj", q, s)
-            q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
-            gu = self.mm(layer, "gate_up_proj", q, s)
+            if fused_norm:
+                gu, res = self.norm_mm(layer, "gate_up_proj", h, res)
+            else:
+                q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
+                gu = self.mm(layer, "gate_up_proj", q, s)
             if fused_down:
                 w, ws = layer["down_proj"]
                 h = fq.silu_mul_quant_mm(gu, w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV,

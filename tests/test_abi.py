@@ -283,6 +283,36 @@ def test_dynamic_quant_entry_validates_on_the_host():
     assert L.i8l_w8a8_mm_dynq(*args) == _lib.OK
 
 
+def test_norm_quant_entry_validates_on_the_host():
+    """i8l_add_rmsnorm_quant_mm: its support rule and argument errors, without a launch."""
+    L = _lib.lib()
+    for m, n, k in ((1, 4096, 2048), (8, 12288, 2048), (8, 6144, 4096), (3, 28672, 4096)):
+        assert L.i8l_add_rmsnorm_quant_mm_supported(m, n, k, None) == _lib.OK, (m, n, k)
+    assert L.i8l_add_rmsnorm_quant_mm_supported(9, 4096, 2048, None) == _lib.UNSUPPORTED
+    assert "up to 8 tokens" in _lib.last_error()
+    assert L.i8l_add_rmsnorm_quant_mm_supported(4, 2048, 6144, None) == _lib.UNSUPPORTED
+    c = _lib.CConfig(16, 16, 256, 8, 4, 2)
+    assert L.i8l_add_rmsnorm_quant_mm_supported(4, 4096, 2048, ctypes.byref(c)) == _lib.OK
+    c = _lib.CConfig(16, 16, 256, 8, 4, 2)                     # K must be warps * bk
+    assert L.i8l_add_rmsnorm_quant_mm_supported(4, 4096, 4096, ctypes.byref(c)) == _lib.UNSUPPORTED
+    c = _lib.CConfig(16, 16, 512, 4, 3, 1)                     # not the persistent form
+    assert L.i8l_add_rmsnorm_quant_mm_supported(4, 4096, 2048, ctypes.byref(c)) == _lib.UNSUPPORTED
+    c = _lib.CConfig(16, 16, 512, 8, 4, 4)                     # four a CU: beyond the LDS
+    assert L.i8l_add_rmsnorm_quant_mm_supported(4, 4096, 4096, ctypes.byref(c)) == _lib.UNSUPPORTED
+    # argument errors come back before anything launches (no pointer is touched)
+    args = [None, None, None, 1e-6, _lib.BF16, 1, None, None, 1, 2048, None, 7, None, 0, None,
+            4096, _lib.BF16, None, 4, 4096, 2048, None, None]
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG and "scale_b" in _lib.last_error()
+    args[11] = 4096
+    args[4] = _lib.F32                                          # fp32 activations
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.UNSUPPORTED
+    args[4], args[6] = _lib.BF16, 1                             # residual_out without residual
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG
+    args[6] = None
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG   # x is NULL
+    assert "required" in _lib.last_error()
+
+
 def test_situ_tune_writes_only_kept_sets_as_table_rows():
     """The in-situ tuner's table rows (reference bench/situ_tune.py:241-246): nothing for a
     set that was not kept; for a kept set, one row per linear at the batch, each with its

@@ -50,7 +50,8 @@ def oracle_step(stack: DecoderStandIn, rows=None) -> tuple[np.ndarray, np.ndarra
     return h, res
 
 
-@pytest.mark.parametrize("m,layers", [(1, 3), (8, 3), (17, 2), (32, 3), (128, 2), (300, 1)])
+@pytest.mark.parametrize("m,layers", [(1, 3), (2, 2), (4, 2), (8, 3), (17, 2), (32, 3), (128, 2),
+                                      (300, 1)])
 @pytest.mark.parametrize("round_silu", [False, True])
 def test_standin_matches_oracle_bit_for_bit(m, layers, round_silu, monkeypatch):
     say(f"standin m={m} layers={layers} round_silu={round_silu}")
@@ -105,3 +106,18 @@ def test_standin_graph_replay_equals_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, again)
         assert not torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("m", [1, 3, 4])
+def test_folded_norm_gives_the_same_step(m):
+    """Up to NORM_MM_FOLD_M tokens the stand-in folds each add+RMSNorm+quant into the
+    projection after it (4 kernels a layer at one token); the step's output and residual
+    stream are the same bits with the fold and without it."""
+    say(f"standin norm fold m={m}")
+    stack = DecoderStandIn(m, layers=3, seed=40 + m)
+    assert stack.fused_norm == (m <= fq.NORM_MM_FOLD_M)
+    h, res = stack.forward(with_residual=True)
+    stack.use_fused_norm = False
+    h0, r0 = stack.forward(with_residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h0) and torch.equal(res, r0)
