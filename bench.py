@@ -809,7 +809,9 @@ def bench_standin(dev) -> dict:
                     "> silu_mul_quant > down, one HIP graph per 28-layer step; folded into one "
                     "launch each where few tokens make it pay: norm+qkv and norm+gate_up up to "
                     f"{fq.NORM_MM_FOLD_M} tokens, quant+o up to {fq.QUANT_MM_MAX_M}, "
-                    f"silu_mul_quant+down up to {fq.SILU_MM_MAX_M}"}
+                    f"silu_mul_quant+down up to {fq.SILU_MM_MAX_M} except at "
+                    f"{fq.SILU_EPI_MIN_M}-{fq.SILU_EPI_MAX_M} tokens, where gate_up writes "
+                    "silu(gate)*up and down quantizes it"}
 
 
 LLAMA_DECODE_M = [1, 4, 16, 64, 128]

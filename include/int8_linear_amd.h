@@ -122,6 +122,30 @@ int i8l_w8a8_mm_ws(const int8_t* a, int64_t stride_am, int64_t stride_ak,
                    const i8l_config* cfg, void* stream);
 
 /*
+ * The gate_up projection with the SiLU-and-mul in its epilogue, for few tokens (M <= 16):
+ *   y = cast(silu(g) * u)  [M, N/2] bf16,  g | u = i8l_w8a8_mm(a, b, scale_a, scale_b, bias)
+ * where g is the product's first N/2 columns and u its last N/2, each rounded to bf16 first
+ * (the gate_up output); round_silu rounds silu(g) to bf16 before the product.  These are the
+ * values i8l_silu_mul_quant quantizes, bit for bit, so i8l_quant_per_token(y) (or the
+ * quantizer folded into the next GEMM, i8l_w8a8_mm_dynq) gives silu_mul_quant's codes and
+ * scales.  Each workgroup's tile pairs gate and up columns, so every value is computed once.
+ * a int8 [M,K] K-contiguous, b the K-contiguous [K,N] view, scale_b per channel [N], bias
+ * none or bf16 [N]; out bf16 with row pitch stride_cm >= N/2, 16-byte aligned.  cfg is a
+ * persistent single-step tile (bm 16, bn 8 or 16, stages 4, K == warps * bk) or NULL.
+ *
+ * Replaces the reference's gate_up_proj _w8a8_mm and the SiLU-and-mul half of
+ * silu_mul_quant (bench/fuse_quant.py:236-240; kernel.py:63-124, fused_quant.py:76-88).
+ */
+int i8l_w8a8_mm_silu_mul(const int8_t* a, int64_t stride_am, const int8_t* b, int64_t stride_bk,
+                         int64_t stride_bn, const float* scale_a, int64_t scale_a_len,
+                         const float* scale_b, int64_t scale_b_len, const void* bias,
+                         int32_t bias_dtype, void* out, int64_t stride_cm, int32_t round_silu,
+                         int64_t M, int64_t N, int64_t K, const i8l_config* cfg, void* stream);
+
+/* Whether i8l_w8a8_mm_silu_mul takes (M,N,K,cfg) (cfg NULL: the library's choice); host-only. */
+int i8l_w8a8_mm_silu_mul_supported(int64_t M, int64_t N, int64_t K, const i8l_config* cfg);
+
+/*
  * i8l_w8a8_mm for callers that cannot allocate: code under HIP graph capture, serving loops
  * and harnesses that forbid allocation.  No counterpart in the reference (its Triton kernel
  * needs no workspace).  Same arguments, validation and results as i8l_w8a8_mm_ws, but a
@@ -264,14 +288,19 @@ int i8l_silu_mul_quant_mm_supported(int64_t M, int64_t N, int64_t K, const i8l_c
  * activation pointer and out 16-byte aligned with 16-byte row pitch.  cfg is a persistent
  * single-step tile of this form (bm 16, bn 8 or 16, bk 256 or 512, 4 or 8 waves, stages 4,
  * K == warps * bk a power of two, group_m workgroups a compute unit) or NULL for the
- * library's choice.
+ * library's choice.  epilogue_act 0 writes the product out [M,N]; 1 and 2 treat b as a
+ * gate_up weight (gate rows [0, N/2), up rows [N/2, N)) and write
+ *   y = cast(silu(g) * u)  [M, N/2] bf16   (2: silu(g) rounded to bf16 first),
+ * the values i8l_silu_mul_quant quantizes, from the bf16 products g, u (bf16 activations and
+ * output, per-channel scale_b, no bias, a residual; else I8L_UNSUPPORTED).
  *
  * Replaces the pair the reference's stand-in issues before its qkv and gate_up projections,
  * add_rmsnorm_quant then _w8a8_mm (bench/fuse_quant.py:226-240 of AshrithaG/int8-linear;
  * int8_linear/fused_quant.py:56-73, 95-110 and kernel.py:202-257).
  */
 int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, const void* weight, float eps,
-                             int32_t act_dtype, int32_t precise_div, void* residual_out,
+                             int32_t act_dtype, int32_t precise_div, int32_t epilogue_act,
+                             void* residual_out,
                              const int8_t* b, int64_t stride_bk, int64_t stride_bn,
                              const float* scale_b, int64_t scale_b_len,
                              const void* bias, int32_t bias_dtype,

@@ -103,14 +103,11 @@ __device__ __forceinline__ float load_sa(const Epi& e, int64_t m) {
   return e.sa[m * (e.sa_per_row ? 1 : 0)];
 }
 
+// The four epilogue values acc * sa * sb (+ bias) in fp32, before the cast (not for raw).
 template <int EK = EK_ANY>
-__device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i acc,
-                                        const Cols4& c, float sam) {
-  const int od = epi_out<EK>(e), bd = epi_bias<EK>(e);
-  if (od == I8L_I32) {
-    *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
-    return;
-  }
+__device__ __forceinline__ void epi_values4(const Epi& e, v4i acc, const Cols4& c, float sam,
+                                            float (&o)[4]) {
+  const int bd = epi_bias<EK>(e);
   float bias[4];
   if (bd == I8L_BF16 || bd == I8L_F16) {
     const uint32_t w[4] = {c.hb.x & 0xffffu, c.hb.x >> 16, c.hb.y & 0xffffu, c.hb.y >> 16};
@@ -121,7 +118,6 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
 #pragma unroll
     for (int r = 0; r < 4; ++r) bias[r] = c.bias[r];
   }
-  float o[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float v = (float)acc[r];
@@ -130,6 +126,18 @@ __device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i 
     if (bd != I8L_DTYPE_NONE) v = v + bias[r];
     o[r] = v;
   }
+}
+
+template <int EK = EK_ANY>
+__device__ __forceinline__ void store4s(const Epi& e, int64_t m, int64_t n, v4i acc,
+                                        const Cols4& c, float sam) {
+  const int od = epi_out<EK>(e);
+  if (od == I8L_I32) {
+    *(v4i*)((int32_t*)e.out + m * e.ldc + n) = acc;
+    return;
+  }
+  float o[4];
+  epi_values4<EK>(e, acc, c, sam, o);
   if (od == I8L_F32) {
     *(float4*)((float*)e.out + m * e.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
   } else {
@@ -171,6 +179,66 @@ __device__ __forceinline__ void store1(const Epi& e, int64_t m, int64_t n, int32
     ((uint16_t*)e.out)[m * e.ldc + n] = f32_to_bf16_bits(v);
   else
     ((uint16_t*)e.out)[m * e.ldc + n] = f32_to_f16_bits(v);
+}
+
+// ------------------------------------------------------------------ SiLU-and-mul
+// What a fused kernel applies to its values: kActPlain nothing; kActSilu the SiLU-and-mul of
+// gate and up values, y = cast(silu(g) * u); kActSiluRound the same with silu(g) rounded to
+// the activation dtype first (reference fused_quant.py:76-88, ROUND_SILU).
+enum { kActPlain = 0, kActSilu = 1, kActSiluRound = 2 };
+
+// silu(g) = g / d with d = 1 + exp(-g) from the canonical exp.  The quotient as rcp(d) with
+// one Newton-Markstein correction and g's sign equals IEEE division for every bf16 and fp16
+// g in (-87, +inf) (the silu_mul_quant kernel's fast form); ieee takes the IEEE division,
+// which a wave holding any other g uses for all of its values.
+__device__ __forceinline__ float silu_canon(float g, bool ieee) {
+  const float d = 1.0f + canon_expf_core(__builtin_amdgcn_fmed3f(-g, -87.5f, 89.5f));
+  if (ieee) return g / d;
+  const float r0 = __builtin_amdgcn_rcpf(d);
+  const float q0 = g * r0;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r0, q0);
+  return __uint_as_float((__float_as_uint(q1) & 0x7fffffffu) | (__float_as_uint(g) & 0x80000000u));
+}
+
+// The SiLU-and-mul epilogue of a decode tile whose MFMA fragment holds the gate columns of a
+// column range in its first rows and the up columns of the same range after them: lane l
+// holds four consecutive columns of one half, and lane l ^ PO the same four columns of the
+// other.  v: the lane's four epilogue values; they are rounded to bf16 (the gate_up output
+// the unfused path would store), swapped with the partner lane, and on the gate lanes turned
+// into y = bf16(silu(g) (rounded for kActSiluRound) * u), the silu_mul_quant kernel's values.
+// Every lane of the wave must call it (cross-lane moves, and the wave-wide IEEE choice).
+template <int ACT, int PO>
+__device__ __forceinline__ void silu_mul_pairs(float (&v)[4], bool gate_lane) {
+  static_assert(ACT == kActSilu || ACT == kActSiluRound, "a SiLU epilogue");
+  float p[4];
+#pragma unroll
+  for (int r = 0; r < 4; r += 2) round_through2<I8L_BF16>(v[r], v[r + 1]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = __shfl_xor(v[r], PO);
+  float gmin = __builtin_inff(), gmax = -__builtin_inff();
+  if (gate_lane)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      gmin = fminf(gmin, v[r]);
+      gmax = fmaxf(gmax, v[r]);
+    }
+  const bool ieee = !__all(gmin > -87.0f && gmax < __builtin_inff());
+  float a[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) a[r] = silu_canon(v[r], ieee);
+  if constexpr (ACT == kActSiluRound) {
+    round_through2<I8L_BF16>(a[0], a[1]);
+    round_through2<I8L_BF16>(a[2], a[3]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = a[r] * p[r];
+}
+
+// Four bf16 values at (m, n) of a row-major bf16 output with row pitch ldc.
+__device__ __forceinline__ void store4_bf16(void* out, int64_t ldc, int64_t m, int64_t n,
+                                            const float (&v)[4]) {
+  *(uint2*)((uint16_t*)out + m * ldc + n) =
+      make_uint2(f32x2_to_bf16x2_bits(v[0], v[1]), f32x2_to_bf16x2_bits(v[2], v[3]));
 }
 
 // Cache policy of the decode schedules' weight copies (global_load_lds): NT, non-temporal.
@@ -285,9 +353,13 @@ hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, cons
 hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                        int64_t ldb, const Epi& e, int64_t K, hipStream_t st);
 bool wldsp_ok(const i8l_config& c, int64_t K);
+bool wldsp_silu_ok(const i8l_config& c, int64_t K);
+hipError_t launch_wldsp_silu(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                             int64_t ldb, const Epi& e, int round_silu, hipStream_t st);
 hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                         int64_t ldb, const Epi& e, hipStream_t st);
 bool dq_ok(const i8l_config& c, int64_t K);
+int dq_max_rows(const i8l_config& c);
 bool default_dq_config(int64_t N, int64_t K, i8l_config* c);
 bool dq_silu_ok(const i8l_config& c, int64_t K);
 bool default_dq_silu_config(int64_t N, int64_t K, i8l_config* c);
@@ -299,7 +371,7 @@ int nq_max_rows();
 hipError_t launch_nq(const i8l_config& c, int act_dtype, const uint16_t* x,
                      const uint16_t* residual, const uint16_t* gamma, float eps,
                      uint16_t* residual_out, const int8_t* b, int64_t ldb, const Epi& e,
-                     float* sa_out, int precise, hipStream_t st);
+                     float* sa_out, int precise, int act, hipStream_t st);
 hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int64_t ldx,
                      const int8_t* b, int64_t ldb, const Epi& e, float* sa_out, int precise,
                      hipStream_t st);

@@ -378,6 +378,12 @@ extern "C" int i8l_w8a8_mm_dynq_supported(int64_t M, int64_t N, int64_t K, const
               c.bm, c.bn, c.bk, c.warps, c.stages, (long long)N, (long long)K);
     return I8L_UNSUPPORTED;
   }
+  // a tile built for fewer than 16 rows a block takes one block of that many
+  if (dq_max_rows(c) < 16 && M > dq_max_rows(c)) {
+    set_error("the dynamic-quant tile %dx%dx%d w%d takes up to %d tokens, got %lld", c.bm, c.bn,
+              c.bk, c.warps, dq_max_rows(c), (long long)M);
+    return I8L_UNSUPPORTED;
+  }
   return I8L_OK;
 }
 
@@ -577,6 +583,7 @@ extern "C" int i8l_add_rmsnorm_quant_mm_supported(int64_t M, int64_t N, int64_t 
 
 extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, const void* weight,
                                         float eps, int32_t act_dtype, int32_t precise_div,
+                                        int32_t epilogue_act,
                                         void* residual_out, const int8_t* b, int64_t stride_bk,
                                         int64_t stride_bn, const float* scale_b,
                                         int64_t scale_b_len, const void* bias,
@@ -617,6 +624,17 @@ extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, con
     set_error("x and the norm weight are required");
     return I8L_INVALID_ARG;
   }
+  if (epilogue_act < 0 || epilogue_act > 2) {
+    set_error("epilogue_act must be 0 (none), 1 (SiLU-and-mul) or 2 (rounded SiLU)");
+    return I8L_INVALID_ARG;
+  }
+  if (epilogue_act != 0 && (act_dtype != I8L_BF16 || out_dtype != I8L_BF16 ||
+                            bias_dtype != I8L_DTYPE_NONE || residual == nullptr ||
+                            scale_b_len != N || N % 2)) {
+    set_error("the SiLU-and-mul epilogue takes bf16 activations and output, a residual, "
+              "per-channel scale_b, no bias and an even N");
+    return I8L_UNSUPPORTED;
+  }
   i8l_config c;
   if (cfg) {
     c = *cfg;
@@ -628,10 +646,11 @@ extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, con
   if (st != I8L_OK) return st;
   if (M == 0 || N == 0) return I8L_OK;
   const int osz = elt_size(out_dtype);
+  const int64_t ncols = epilogue_act ? N / 2 : N;   // the output's columns
   const bool layout = stride_bk == 1 && aligned16(b) && stride_bn % 16 == 0 &&
                       stride_bn <= INT32_MAX / 32 && aligned16(x) && aligned16(weight) &&
                       (residual == nullptr || (aligned16(residual) && aligned16(residual_out))) &&
-                      aligned16(out) && (stride_cm * osz) % 16 == 0 && stride_cm >= N &&
+                      aligned16(out) && (stride_cm * osz) % 16 == 0 && stride_cm >= ncols &&
                       N % 4 == 0 && (scale_b_len == 1 || aligned16(scale_b)) &&
                       (bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
   if (!layout) {
@@ -652,9 +671,112 @@ extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, con
   e.N = (int)N;
   const hipError_t err = launch_nq(c, act_dtype, (const uint16_t*)x, (const uint16_t*)residual,
                                    (const uint16_t*)weight, eps, (uint16_t*)residual_out, b,
-                                   stride_bn, e, scale_a_out, precise_div ? 1 : 0,
+                                   stride_bn, e, scale_a_out, precise_div ? 1 : 0, epilogue_act,
                                    (hipStream_t)stream);
   return hip_status(err, "i8l_add_rmsnorm_quant_mm launch");
+}
+
+// ------------------------------------------------------------------ GEMM + SiLU-and-mul
+// The untuned choice: the persistent single-step tile (one 16-row block) with 16 columns a
+// tile (8 gate and 8 up), 4 waves of 512-byte slices for K = 2048 and two workgroups a
+// compute unit, else the first built form that takes K.
+static bool default_silu_config(int64_t N, int64_t K, i8l_config* c) {
+  static const int pref[][4] = {{16, 512, 4, 2}, {16, 256, 8, 2}, {16, 128, 16, 1},
+                                {16, 512, 8, 1}, {16, 256, 16, 1}, {16, 1024, 4, 1},
+                                {8, 512, 4, 2},  {8, 256, 8, 2},   {8, 128, 16, 1}};
+  for (const auto& p : pref) {
+    const i8l_config t{16, p[0], p[1], p[2], 4, p[3]};
+    if (N % t.bn == 0 && wldsp_silu_ok(t, K)) {
+      *c = t;
+      return true;
+    }
+  }
+  return false;
+}
+
+extern "C" int i8l_w8a8_mm_silu_mul_supported(int64_t M, int64_t N, int64_t K,
+                                              const i8l_config* cfg) {
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_silu_config(N, K, &c)) {
+    set_error("no built SiLU-epilogue tile takes K=%lld, N=%lld", (long long)K, (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  if (M < 0 || M > 16 || N > INT32_MAX || K > INT32_MAX) {
+    set_error("the SiLU-and-mul epilogue takes up to 16 tokens, got %lld", (long long)M);
+    return I8L_UNSUPPORTED;
+  }
+  if (c.bn <= 0 || N % c.bn || !wldsp_silu_ok(c, K)) {
+    set_error("config %dx%dx%d w%d s%d g%d is not a built SiLU-epilogue tile for N=%lld K=%lld",
+              c.bm, c.bn, c.bk, c.warps, c.stages, c.group_m, (long long)N, (long long)K);
+    return I8L_UNSUPPORTED;
+  }
+  return I8L_OK;
+}
+
+extern "C" int i8l_w8a8_mm_silu_mul(const int8_t* a, int64_t stride_am, const int8_t* b,
+                                    int64_t stride_bk, int64_t stride_bn, const float* scale_a,
+                                    int64_t scale_a_len, const float* scale_b,
+                                    int64_t scale_b_len, const void* bias, int32_t bias_dtype,
+                                    void* out, int64_t stride_cm, int32_t round_silu,
+                                    int64_t M, int64_t N, int64_t K, const i8l_config* cfg,
+                                    void* stream) {
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("negative size M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    return I8L_INVALID_ARG;
+  }
+  if (scale_a_len != 1 && scale_a_len != M) {
+    set_error("scale_a has %lld values for M=%lld", (long long)scale_a_len, (long long)M);
+    return I8L_INVALID_ARG;
+  }
+  if (scale_b_len != N || N % 2) {
+    set_error("the SiLU-and-mul epilogue needs N even and N per-channel scales (got %lld "
+              "for N=%lld)", (long long)scale_b_len, (long long)N);
+    return I8L_INVALID_ARG;
+  }
+  if (bias_dtype != I8L_DTYPE_NONE && bias_dtype != I8L_BF16) {
+    set_error("the SiLU-and-mul epilogue takes no bias or a bf16 bias (code %d)", bias_dtype);
+    return I8L_UNSUPPORTED;
+  }
+  if ((bias_dtype == I8L_DTYPE_NONE) != (bias == nullptr)) {
+    set_error("bias pointer and bias dtype disagree");
+    return I8L_INVALID_ARG;
+  }
+  i8l_config c;
+  if (cfg) {
+    c = *cfg;
+  } else if (!default_silu_config(N, K, &c)) {
+    set_error("no built SiLU-epilogue tile takes K=%lld, N=%lld", (long long)K, (long long)N);
+    return I8L_UNSUPPORTED;
+  }
+  const int st = i8l_w8a8_mm_silu_mul_supported(M, N, K, &c);
+  if (st != I8L_OK) return st;
+  if (M == 0 || N == 0) return I8L_OK;
+  const bool layout = stride_bk == 1 && aligned16(b) && stride_bn % 16 == 0 &&
+                      stride_bn <= INT32_MAX / 64 && aligned16(a) && stride_am % 16 == 0 &&
+                      stride_am <= INT32_MAX / 128 && aligned16(out) && (stride_cm * 2) % 16 == 0 &&
+                      stride_cm >= N / 2 && aligned16(scale_b) &&
+                      (bias_dtype == I8L_DTYPE_NONE || aligned16(bias));
+  if (!layout) {
+    set_error("the SiLU-epilogue path needs K-contiguous 16-byte aligned operands");
+    return I8L_UNSUPPORTED;
+  }
+  Epi e;
+  e.sa = scale_a;
+  e.sb = scale_b;
+  e.bias = bias;
+  e.out = out;
+  e.ldc = stride_cm;
+  e.sa_per_row = scale_a_len == M && M > 1;
+  e.sb_per_col = 1;
+  e.bias_dtype = bias_dtype;
+  e.out_dtype = I8L_BF16;
+  e.M = (int)M;
+  e.N = (int)N;
+  const hipError_t err = launch_wldsp_silu(c, a, stride_am, b, stride_bn, e, round_silu ? 1 : 0,
+                                           (hipStream_t)stream);
+  return hip_status(err, "i8l_w8a8_mm_silu_mul launch");
 }
 
 // ------------------------------------------------------------------ allocation-free entry

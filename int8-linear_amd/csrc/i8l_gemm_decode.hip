@@ -579,7 +579,13 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
 // here A is read once per workgroup.  Each wave reads only its own weight slices, so a
 // buffer is refilled as soon as the wave's own MFMAs have consumed it; the reduction area
 // is shared and is fenced by a barrier on each side.
-template <int MT, int NC, int KS, int W, int EK>
+//
+// ACT kActSilu / kActSiluRound: the gate_up projection with the SiLU-and-mul epilogue.  The
+// weight's first N/2 rows are the gate, the last N/2 the up projection; tile t takes gate rows
+// [t*H, (t+1)*H) and the same up rows (H = NC/2) into the fragment's first and last H rows,
+// and the epilogue writes y = silu(gate) * up, [M, N/2] bf16 (silu_mul_pairs), instead of the
+// [M, N] product.
+template <int MT, int NC, int KS, int W, int EK, int ACT = kActPlain>
 __global__ void __launch_bounds__(64 * W)
 gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
             int64_t ldb, Epi e) {
@@ -596,6 +602,10 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   constexpr int FR = MT * NF;
   static_assert(NF * NCF == NC, "the tile must be whole column fragments");
   static_assert(FR <= W, "every fragment needs a storing wave");
+  constexpr bool SILU = ACT != kActPlain;
+  static_assert(!SILU || (MT == 1 && NF == 1 && EK != EK_ANY),
+                "the SiLU epilogue takes one fragment of bf16 output");
+  constexpr int H = NC / 2;                  // SiLU: gate (and up) columns of a tile
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
@@ -610,14 +620,27 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   const int ldb32 = (int)ldb;
 
   auto dma = [&](int ct, int8_t* wb) {
-    const int8_t* Bw = B + (int64_t)ct * NC * ldb + kw;
     lds_i8_t* dst = (lds_i8_t*)wb;
+    if constexpr (SILU) {
+      // tile row r: gate row ct*H + r for r < H, else up row N/2 + ct*H + r - H
+      const int8_t* Bg = B + (int64_t)ct * H * ldb + kw;
+      const int8_t* Bu = Bg + (int64_t)(e.N / 2) * ldb - (int64_t)H * ldb;
 #pragma unroll
-    for (int t = 0; t < NI; ++t) {
-      const int o = t * 1024 + 16 * lane;
-      const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
-      __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
-                                       16, 0, kWeightCpol);
+      for (int t = 0; t < NI; ++t) {
+        const int o = t * 1024 + 16 * lane;
+        const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+        __builtin_amdgcn_global_load_lds((const void*)((r < H ? Bg : Bu) + (r * ldb32 + 16 * c)),
+                                         dst + t * 1024, 16, 0, kWeightCpol);
+      }
+    } else {
+      const int8_t* Bw = B + (int64_t)ct * NC * ldb + kw;
+#pragma unroll
+      for (int t = 0; t < NI; ++t) {
+        const int o = t * 1024 + 16 * lane;
+        const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
+        __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
+                                         16, 0, kWeightCpol);
+      }
     }
   };
 
@@ -640,7 +663,10 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   for (int it = 0; ct < tiles; ++it, ct += gridDim.x) {
     int8_t* const cur = (it & 1) ? wb1 : wb0;
     const int64_t n0 = (int64_t)ct * NC;
-    const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+    const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
+    // SiLU: gate lanes (cq < H) read gate columns ct*H + cq, up lanes up columns N/2 + ...
+    const int64_t ncol = SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
+                              : n0 + NCF * (wave % NF) + cq;
     Cols4 cl;
     if (wave < FR) cl = load_cols4<EK>(e, ncol);
     const bool more = ct + (int)gridDim.x < tiles;  // uniform over the workgroup
@@ -679,7 +705,14 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
       v4i sum = red[wave * 64 + lane];
 #pragma unroll
       for (int w = 1; w < W; ++w) sum += red[(w * FR + wave) * 64 + lane];
-      if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
+      if constexpr (SILU) {
+        float v[4];
+        epi_values4<EK>(e, sum, cl, sam, v);
+        silu_mul_pairs<ACT, 4 * H>(v, cq < H);
+        if (mrow < e.M && cq < H && 4 * grp < NCF) store4_bf16(e.out, e.ldc, mrow, ct * H + cq, v);
+      } else {
+        if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
+      }
     }
     __syncthreads();  // the partials of the next tile overwrite the reduction area
   }
@@ -705,7 +738,6 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // and a correctly rounded quotient, rounded to the activation dtype first for kActSiluRound;
 // these are the silu_mul_quant kernel's values, so the output equals silu_mul_quant followed
 // by w8a8_mm bit for bit (reference fused_quant.py:76-88 then kernel.py:63-124).
-enum { kActPlain = 0, kActSilu = 1, kActSiluRound = 2 };
 
 template <int NC, int KS, int W, int P, int EK, int DT, int ACT>
 __global__ void __launch_bounds__(64 * W)
@@ -787,19 +819,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
   // correction and g's sign, which equals IEEE division for every bf16 and fp16 g in
   // (-87, +inf) (the silu_mul_quant kernel's fast form); a wave holding any other g takes
   // IEEE division for all of its values.
-  auto silu = [&](float g, bool ieee) -> float {
-    const float d = 1.0f + canon_expf_core(__builtin_amdgcn_fmed3f(-g, -87.5f, 89.5f));
-    float a;
-    if (ieee) {
-      a = g / d;
-    } else {
-      const float r0 = __builtin_amdgcn_rcpf(d);
-      const float q0 = g * r0;
-      const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, g), r0, q0);
-      a = __uint_as_float((__float_as_uint(q1) & 0x7fffffffu) | (__float_as_uint(g) & 0x80000000u));
-    }
-    return a;
-  };
+  auto silu = [&](float g, bool ieee) -> float { return silu_canon(g, ieee); };
   auto fill = [&](bool ieee) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -1297,10 +1317,10 @@ int cu_count() {
   return n;
 }
 
-template <int MT, int NC, int KS, int W, int EK>
+template <int MT, int NC, int KS, int W, int EK, int ACT = kActPlain>
 hipError_t launch_wldsp_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, int per_cu, hipStream_t st) {
-  auto kern = gemm_wlds1p<MT, NC, KS, W, EK>;
+  auto kern = gemm_wlds1p<MT, NC, KS, W, EK, ACT>;
   const size_t shm = wldsp_lds_bytes(MT, NC, KS, W);
   static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
   lds_opt_in((const void*)kern, shm, lds_done);
@@ -1338,6 +1358,40 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
   return hipErrorInvalidValue;
 }
 
+// The persistent single-step tiles with the SiLU-and-mul epilogue (one 16-row block, 8 or 16
+// columns a tile, bf16 output with no bias or a bf16 bias).
+bool wldsp_silu_ok(const i8l_config& c, int64_t K) {
+  return wldsp_ok(c, K) && c.bm == 16 && (c.bn == 8 || c.bn == 16);
+}
+
+template <int NC, int KS, int W, int ACT>
+hipError_t launch_wldsp_silu_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                               const Epi& e, int per_cu, hipStream_t st) {
+  switch (epi_kind(e)) {
+    case EK_BF16: return launch_wldsp_k<1, NC, KS, W, EK_BF16, ACT>(a, lda, b, ldb, e, per_cu, st);
+    case EK_BF16_BBF16:
+      return launch_wldsp_k<1, NC, KS, W, EK_BF16_BBF16, ACT>(a, lda, b, ldb, e, per_cu, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_wldsp_silu(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
+                             int64_t ldb, const Epi& e, int round_silu, hipStream_t st) {
+  const int nc = c.bn, ks = c.bk / 64, w = c.warps;
+  if (c.bm != 16) return hipErrorInvalidValue;
+#define I8L_WLDSP_SILU(NC_, KS_, W_)                                                        \
+  if (nc == NC_ && ks == KS_ && w == W_)                                                     \
+    return round_silu                                                                        \
+        ? launch_wldsp_silu_t<NC_, KS_, W_, kActSiluRound>(a, lda, b, ldb, e, c.group_m, st) \
+        : launch_wldsp_silu_t<NC_, KS_, W_, kActSilu>(a, lda, b, ldb, e, c.group_m, st);
+  I8L_WLDSP_SILU(16, 2, 16) I8L_WLDSP_SILU(16, 4, 16) I8L_WLDSP_SILU(16, 4, 8)
+  I8L_WLDSP_SILU(16, 8, 8) I8L_WLDSP_SILU(8, 2, 16) I8L_WLDSP_SILU(8, 4, 16)
+  I8L_WLDSP_SILU(8, 8, 8) I8L_WLDSP_SILU(8, 16, 4) I8L_WLDSP_SILU(16, 16, 4)
+  I8L_WLDSP_SILU(8, 8, 4) I8L_WLDSP_SILU(16, 8, 4)
+#undef I8L_WLDSP_SILU
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, const int8_t* b,
                          int64_t ldb, const Epi& e, int K, hipStream_t st) {
   const int mt = c.bm / 16, bn = c.bn, W = c.warps, ks = K / (64 * W);
@@ -1356,7 +1410,10 @@ hipError_t launch_stream(const i8l_config& c, const int8_t* a, int64_t lda, cons
 struct DqTile {
   int nc, ks, w;
 };
-constexpr DqTile kDq[] = {{8, 2, 16}, {16, 2, 16}, {32, 2, 16}, {8, 4, 16}, {16, 4, 16}};
+// {8, 8, 12}: 12 waves of 512-byte slices for K = 6144 (the down projection fed by the
+// gate_up GEMM's SiLU-and-mul epilogue).
+constexpr DqTile kDq[] = {{8, 2, 16}, {16, 2, 16}, {32, 2, 16}, {8, 4, 16}, {16, 4, 16},
+                          {8, 8, 12}};
 // The SiLU-and-mul form's tiles (gate_up rows of 2K values feeding K = 64 * KS * W): 12 waves
 // of 512-byte slices take Qwen3-1.7B's K = 6144 (a slice of 384 bytes would not split the
 // 8-value chunks of a row over the lanes).  One 16-token row block with at most 8 valid
@@ -1371,6 +1428,10 @@ size_t dq_lds_bytes(int nc, int ks, int W) {
          (size_t)W * 16 * 64 * ks;
 }
 
+// Token rows a dynamic-quant tile takes: a 16-row block, built with up to 8 passes of
+// 64 / (S/8) rows (so 8 rows for 512-byte slices).
+int dq_max_rows(const i8l_config& c) { return std::min(16, 8 * (512 / c.bk)); }
+
 bool dq_ok(const i8l_config& c, int64_t K) {
   if (c.stages != 3 || c.bm != 16) return false;
   for (auto t : kDq)
@@ -1380,7 +1441,7 @@ bool dq_ok(const i8l_config& c, int64_t K) {
 }
 
 // The untuned choice: 16 waves that take K in one step each, 16 columns a workgroup (8 for
-// narrow N).
+// narrow N); K = 6144 takes 12 waves of 512 bytes and 8 columns.
 bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
   const int nc = (N % 16 == 0 && N / 16 >= 256) ? 16 : 8;
   for (int ks : {2, 4}) {
@@ -1389,6 +1450,11 @@ bool default_dq_config(int64_t N, int64_t K, i8l_config* c) {
       *c = t;
       return true;
     }
+  }
+  const i8l_config t{16, 8, 512, 12, 3, 1};
+  if (N % 8 == 0 && dq_ok(t, K)) {
+    *c = t;
+    return true;
   }
   return false;
 }
@@ -1481,6 +1547,7 @@ hipError_t launch_dq(const i8l_config& c, int act_dtype, const uint16_t* x, int6
     return launch_dq_t<NC_, KS_, W_, kActPlain, 16>(act_dtype, x, ldx, 0, b, ldb, e, sa_out, \
                                                     precise, st);
   I8L_DQ(8, 2, 16) I8L_DQ(16, 2, 16) I8L_DQ(32, 2, 16) I8L_DQ(8, 4, 16) I8L_DQ(16, 4, 16)
+  I8L_DQ(8, 8, 12)
 #undef I8L_DQ
   return hipErrorInvalidValue;
 }

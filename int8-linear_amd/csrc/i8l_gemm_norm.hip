@@ -45,8 +45,11 @@ __device__ __forceinline__ void unpack8_act(const uint4& v, float* o) {
 
 // NC columns a tile, K slices of S = 64*KS bytes over W waves (K = W*S), P passes of RPP
 // rows over the token rows (at most 8), DT the activation dtype (the norm weight's too),
-// RES whether a residual is added (else the first layer's plain RMSNorm).
-template <int NC, int KS, int W, int P, int EK, int DT, bool RES>
+// RES whether a residual is added (else the first layer's plain RMSNorm).  ACT kActSilu /
+// kActSiluRound: the gate_up projection with the SiLU-and-mul epilogue of gemm_wlds1p
+// (tile t: gate rows [t*H, (t+1)*H) and the same up rows, H = NC/2; y = silu(gate) * up,
+// [M, N/2] bf16).
+template <int NC, int KS, int W, int P, int EK, int DT, bool RES, int ACT = kActPlain>
 __global__ void __launch_bounds__(64 * W)
 gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
                const uint16_t* __restrict__ G, float eps, uint16_t* __restrict__ rout,
@@ -70,6 +73,9 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   static_assert((W & (W - 1)) == 0, "the waves' slices must be nodes of the row's tree");
   static_assert(P >= 1 && P * RPP <= 16, "the passes cover at most one 16-row block");
   static_assert(NC >= 8, "the code tile of up to 8 rows lives in a weight buffer");
+  constexpr bool SILU = ACT != kActPlain;
+  static_assert(!SILU || (NF == 1 && EK != EK_ANY), "the SiLU epilogue takes bf16 output");
+  constexpr int H = NC / 2;                 // SiLU: gate (and up) columns of a tile
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
   const int lane = threadIdx.x & 63;
@@ -87,14 +93,18 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   const int ldb32 = (int)ldb;
 
   auto dma = [&](int ct, int8_t* wb) {
-    const int8_t* Bw = B + (int64_t)ct * NC * ldb + kw;
     lds_i8_t* dst = (lds_i8_t*)wb;
+    // tile row r: weight row ct*NC + r; SiLU: gate row ct*H + r for r < H, else up row
+    // N/2 + ct*H + r - H
+    const int8_t* Bw = B + (int64_t)ct * (SILU ? H : NC) * ldb + kw;
+    const int8_t* Bu = SILU ? Bw + (int64_t)(e.N / 2) * ldb - (int64_t)H * ldb : Bw;
 #pragma unroll
     for (int t = 0; t < NI; ++t) {
       const int o = t * 1024 + 16 * lane;
       const int r = o / S, c = ((o % S) / 16) ^ (r & SWM);
-      __builtin_amdgcn_global_load_lds((const void*)(Bw + (r * ldb32 + 16 * c)), dst + t * 1024,
-                                       16, 0, kWeightCpol);
+      __builtin_amdgcn_global_load_lds((const void*)((SILU && r >= H ? Bu : Bw) +
+                                                     (r * ldb32 + 16 * c)),
+                                       dst + t * 1024, 16, 0, kWeightCpol);
     }
   };
 
@@ -229,8 +239,9 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   int ct = blockIdx.x;
   for (int it = 0; ct < tiles; ++it, ct += gridDim.x) {
     int8_t* const cur = (it & 1) ? wb1 : wb0;
-    const int64_t n0 = (int64_t)ct * NC;
-    const int64_t ncol = n0 + NCF * (wave % NF) + 4 * (grp & (NCF / 4 - 1));
+    const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
+    const int64_t ncol = SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
+                              : (int64_t)ct * NC + NCF * (wave % NF) + cq;
     Cols4 cl;
     if (wave < NF) cl = load_cols4<EK>(e, ncol);
     const bool more = ct + (int)gridDim.x < tiles;  // uniform over the workgroup
@@ -263,7 +274,14 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       v4i sum = red[wave * 64 + lane];
 #pragma unroll
       for (int w = 1; w < W; ++w) sum += red[(w * NF + wave) * 64 + lane];
-      if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, r16, ncol, sum, cl, sam);
+      if constexpr (SILU) {
+        float v[4];
+        epi_values4<EK>(e, sum, cl, sam, v);
+        silu_mul_pairs<ACT, 4 * H>(v, cq < H);
+        if (r16 < mb && cq < H && 4 * grp < NCF) store4_bf16(e.out, e.ldc, r16, ct * H + cq, v);
+      } else {
+        if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, r16, ncol, sum, cl, sam);
+      }
     }
     __syncthreads();  // the partials of the next tile overwrite the reduction area
   }
@@ -320,11 +338,11 @@ bool default_nq_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   return false;
 }
 
-template <int NC, int KS, int W, int P, int EK, int DT, bool RES>
+template <int NC, int KS, int W, int P, int EK, int DT, bool RES, int ACT = kActPlain>
 hipError_t launch_nq_k(const uint16_t* x, const uint16_t* res, const uint16_t* gamma, float eps,
                        uint16_t* rout, const int8_t* b, int64_t ldb, const Epi& e,
                        float* sa_out, int precise, int per_cu, hipStream_t st) {
-  auto kern = gemm_wlds1p_nq<NC, KS, W, P, EK, DT, RES>;
+  auto kern = gemm_wlds1p_nq<NC, KS, W, P, EK, DT, RES, ACT>;
   const size_t shm = nq_lds_bytes(NC, KS, W);
   static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
   lds_opt_in((const void*)kern, shm, lds_done);
@@ -338,7 +356,19 @@ hipError_t launch_nq_k(const uint16_t* x, const uint16_t* res, const uint16_t* g
 template <int NC, int KS, int W, int P, int DT, bool RES>
 hipError_t launch_nq_e(const uint16_t* x, const uint16_t* res, const uint16_t* gamma, float eps,
                        uint16_t* rout, const int8_t* b, int64_t ldb, const Epi& e,
-                       float* sa_out, int precise, int per_cu, hipStream_t st) {
+                       float* sa_out, int precise, int per_cu, int act, hipStream_t st) {
+  // the SiLU epilogue: bf16 activations and output, a residual, no bias (the MLP's gate_up)
+  if constexpr (DT == I8L_BF16 && RES) {
+    if (act != kActPlain) {
+      if (epi_kind(e) != EK_BF16) return hipErrorInvalidValue;
+      return act == kActSiluRound
+          ? launch_nq_k<NC, KS, W, P, EK_BF16, DT, RES, kActSiluRound>(
+                x, res, gamma, eps, rout, b, ldb, e, sa_out, precise, per_cu, st)
+          : launch_nq_k<NC, KS, W, P, EK_BF16, DT, RES, kActSilu>(
+                x, res, gamma, eps, rout, b, ldb, e, sa_out, precise, per_cu, st);
+    }
+  }
+  if (act != kActPlain) return hipErrorInvalidValue;
   if constexpr (DT == I8L_BF16) {
     switch (epi_kind(e)) {
       case EK_BF16:
@@ -356,30 +386,35 @@ hipError_t launch_nq_e(const uint16_t* x, const uint16_t* res, const uint16_t* g
 }
 
 // Passes: ceil(rows / RPP) rounded up to a power of two, for at most kNqMaxRows rows.
+template <int NC, int KS, int W, int P>
+hipError_t launch_nq_p(int act_dtype, const uint16_t* x, const uint16_t* res,
+                       const uint16_t* gamma, float eps, uint16_t* rout, const int8_t* b,
+                       int64_t ldb, const Epi& e, float* sa_out, int precise, int per_cu,
+                       int act, hipStream_t st) {
+  if (act_dtype == I8L_F16)
+    return res ? launch_nq_e<NC, KS, W, P, I8L_F16, true>(x, res, gamma, eps, rout, b, ldb, e,
+                                                          sa_out, precise, per_cu, act, st)
+               : launch_nq_e<NC, KS, W, P, I8L_F16, false>(x, res, gamma, eps, rout, b, ldb, e,
+                                                           sa_out, precise, per_cu, act, st);
+  return res ? launch_nq_e<NC, KS, W, P, I8L_BF16, true>(x, res, gamma, eps, rout, b, ldb, e,
+                                                         sa_out, precise, per_cu, act, st)
+             : launch_nq_e<NC, KS, W, P, I8L_BF16, false>(x, res, gamma, eps, rout, b, ldb, e,
+                                                          sa_out, precise, per_cu, act, st);
+}
+
 template <int NC, int KS, int W>
 hipError_t launch_nq_t(int act_dtype, const uint16_t* x, const uint16_t* res,
                        const uint16_t* gamma, float eps, uint16_t* rout, const int8_t* b,
                        int64_t ldb, const Epi& e, float* sa_out, int precise, int per_cu,
-                       hipStream_t st) {
+                       int act, hipStream_t st) {
   constexpr int RPP = 64 / (8 * KS);
   const int need = (e.M + RPP - 1) / RPP;
+  // P = 1, 2, 4, 8 where P passes are the fewest that cover some row count up to the maximum
 #define I8L_NQ_P(P_)                                                                         \
-  if constexpr (P_ * RPP <= 2 * kNqMaxRows && (P_ == 1 || (P_ / 2) * RPP < kNqMaxRows))      \
-    if (need <= P_) {                                                                        \
-      if (act_dtype == I8L_F16)                                                              \
-        return res ? launch_nq_e<NC, KS, W, P_, I8L_F16, true>(x, res, gamma, eps, rout, b,  \
-                                                               ldb, e, sa_out, precise,      \
-                                                               per_cu, st)                   \
-                   : launch_nq_e<NC, KS, W, P_, I8L_F16, false>(x, res, gamma, eps, rout, b, \
-                                                                ldb, e, sa_out, precise,     \
-                                                                per_cu, st);                 \
-      return res ? launch_nq_e<NC, KS, W, P_, I8L_BF16, true>(x, res, gamma, eps, rout, b,   \
-                                                              ldb, e, sa_out, precise,       \
-                                                              per_cu, st)                    \
-                 : launch_nq_e<NC, KS, W, P_, I8L_BF16, false>(x, res, gamma, eps, rout, b,  \
-                                                               ldb, e, sa_out, precise,      \
-                                                               per_cu, st);                  \
-    }
+  if constexpr (P_ == 1 || (P_ / 2) * RPP < kNqMaxRows)                                      \
+    if (need <= P_)                                                                          \
+      return launch_nq_p<NC, KS, W, P_>(act_dtype, x, res, gamma, eps, rout, b, ldb, e,      \
+                                        sa_out, precise, per_cu, act, st);
   I8L_NQ_P(1) I8L_NQ_P(2) I8L_NQ_P(4) I8L_NQ_P(8)
 #undef I8L_NQ_P
   return hipErrorInvalidValue;
@@ -388,12 +423,12 @@ hipError_t launch_nq_t(int act_dtype, const uint16_t* x, const uint16_t* res,
 hipError_t launch_nq(const i8l_config& c, int act_dtype, const uint16_t* x,
                      const uint16_t* residual, const uint16_t* gamma, float eps,
                      uint16_t* residual_out, const int8_t* b, int64_t ldb, const Epi& e,
-                     float* sa_out, int precise, hipStream_t st) {
+                     float* sa_out, int precise, int act, hipStream_t st) {
   const int nc = c.bn, ks = c.bk / 64, w = c.warps;
 #define I8L_NQ(NC_, KS_, W_)                                                                 \
   if (nc == NC_ && ks == KS_ && w == W_)                                                     \
     return launch_nq_t<NC_, KS_, W_>(act_dtype, x, residual, gamma, eps, residual_out, b,    \
-                                     ldb, e, sa_out, precise, c.group_m, st);
+                                     ldb, e, sa_out, precise, c.group_m, act, st);
   I8L_NQ(16, 8, 4) I8L_NQ(16, 4, 8) I8L_NQ(8, 8, 4) I8L_NQ(8, 4, 8) I8L_NQ(16, 8, 8)
   I8L_NQ(8, 8, 8)
 #undef I8L_NQ

@@ -280,7 +280,8 @@ def add_rmsnorm_quant_mm(x: torch.Tensor, residual: torch.Tensor | None, weight:
                          eps: float, b_q: torch.Tensor, scale_b: torch.Tensor,
                          out_dtype: torch.dtype = torch.bfloat16,
                          bias: torch.Tensor | None = None, precise_div: bool = True, *,
-                         config=None, return_scale: bool = False):
+                         config=None, return_scale: bool = False, silu_mul: bool = False,
+                         round_silu: bool = False):
     """add_rmsnorm_quant(x, residual, weight, eps) followed by w8a8_mm, as one kernel, for up
     to NORM_MM_MAX_M tokens: (out [M, N], residual_out [M, K] or None), and the per-token
     scales [M, 1] last with return_scale.
@@ -289,8 +290,10 @@ def add_rmsnorm_quant_mm(x: torch.Tensor, residual: torch.Tensor | None, weight:
     in one launch): out = w8a8_mm(q, b_q, s, scale_b, out_dtype, bias) with (q, s,
     residual_out) = add_rmsnorm_quant(x, residual, weight, eps, precise_div).  x and residual
     are contiguous bf16/fp16 [M, K], weight [K] of x's dtype, b_q the K-contiguous [K, N]
-    view of an [N, K] weight.  Raises NotSupported for more tokens, a K no built tile takes,
-    or layouts the fused kernel does not read (the caller then makes the two calls).
+    view of an [N, K] weight.  With silu_mul, b_q is a gate_up weight and out is
+    y = silu(gate) * up [M, N/2] as w8a8_mm_silu_mul gives it (bf16, a residual, no bias).
+    Raises NotSupported for more tokens, a K no built tile takes, or layouts the fused kernel
+    does not read (the caller then makes the two calls).
     """
     from int8_linear.kernel import Config, _cconfig
     if x.dim() != 2 or b_q.dim() != 2 or x.shape[1] != b_q.shape[0]:
@@ -312,13 +315,15 @@ def add_rmsnorm_quant_mm(x: torch.Tensor, residual: torch.Tensor | None, weight:
             raise NotSupported("residual must be a contiguous tensor of x's shape and dtype")
     N, sb, bias, bias_code, out_code = _mm_operands(x, b_q, scale_b, bias, out_dtype,
                                                     "add_rmsnorm_quant_mm")
-    out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    out = torch.empty((M, N // 2 if silu_mul else N), dtype=out_dtype, device=x.device)
     rout = torch.empty_like(x) if residual is not None else None
     s = torch.empty((M, 1), dtype=torch.float32, device=x.device) if return_scale else None
     cfg = _cconfig(config) if isinstance(config, Config) else None
+    epi = (2 if round_silu else 1) if silu_mul else 0
     status = _lib.lib().i8l_add_rmsnorm_quant_mm(
         x.data_ptr(), residual.data_ptr() if residual is not None else None, weight.data_ptr(),
-        float(eps), act, int(bool(precise_div)), rout.data_ptr() if rout is not None else None,
+        float(eps), act, int(bool(precise_div)), epi,
+        rout.data_ptr() if rout is not None else None,
         b_q.data_ptr(), b_q.stride(0), b_q.stride(1), sb.data_ptr(), sb.numel(),
         bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
         out.stride(0), out_code, s.data_ptr() if s is not None else None, M, N, K, cfg,
@@ -334,6 +339,63 @@ def add_rmsnorm_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
         return False
     cfg = _cconfig(config) if isinstance(config, Config) else None
     return _lib.lib().i8l_add_rmsnorm_quant_mm_supported(m, n, k, cfg) == _lib.OK
+
+
+# Token counts for which the decoder stand-in computes the SiLU-and-mul in gate_up_proj's
+# epilogue and folds the quantizer into down_proj (the kernel takes up to 16 tokens).
+# Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with / without:
+# 21.63 / 21.54 at 1 token, 23.00 / 23.59 at 2, 26.33 / 26.92 at 3, 27.67 / 27.57 at 4,
+# 30.87 / 29.37 at 5, 33.00 / 30.32 at 8: the paired gate/up epilogue costs gate_up 0.6-0.8 us
+# (6.58 against 5.91 at one token), which the cheaper down_proj prologue repays only at 2-3
+# tokens, and from 5 tokens every CU repeats the quantizer of 6144 values a row.
+SILU_EPI_MIN_M = 2
+SILU_EPI_MAX_M = 3
+
+
+def w8a8_mm_silu_mul(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
+                     scale_b: torch.Tensor, round_silu: bool = False,
+                     bias: torch.Tensor | None = None, *, config=None) -> torch.Tensor:
+    """The gate_up projection with the SiLU-and-mul in its epilogue, for few tokens (up to
+    16): y = silu(g) * u, [M, N/2] bf16, where g | u = w8a8_mm(a_q, b_q, scale_a, scale_b,
+    bf16, bias) split at N/2.
+
+    y is bit for bit the values silu_mul_quant(g | u, round_silu=round_silu) quantizes
+    (reference fused_quant.py:76-88), so quant_per_token(y), or quant_mm(y, ...) into the
+    down projection, gives its codes and scales; each value is computed once, by the
+    workgroup whose tile holds that gate and up column.  b_q is the K-contiguous [K, N] view
+    of the [N, K] gate_up weight (gate rows first), scale_b per channel [N], bias None or
+    bf16 [N].  Raises NotSupported for more tokens or what the kernel does not take.
+    """
+    from int8_linear.kernel import Config, _cconfig
+    if a_q.dtype != torch.int8 or b_q.dtype != torch.int8:
+        raise NotSupported(f"int8 operands only, got {a_q.dtype} and {b_q.dtype}")
+    if a_q.dim() != 2 or b_q.dim() != 2 or a_q.shape[1] != b_q.shape[0]:
+        raise ValueError(f"cannot multiply {tuple(a_q.shape)} by {tuple(b_q.shape)}")
+    if not (a_q.is_cuda and a_q.stride(1) == 1):
+        raise NotSupported("a_q must be a K-contiguous HIP tensor")
+    M, K = a_q.shape
+    N, sb, bias, bias_code, _ = _mm_operands(a_q, b_q, scale_b, bias, torch.bfloat16,
+                                             "w8a8_mm_silu_mul")
+    sa = scale_a.reshape(-1).contiguous()
+    if sa.dtype != torch.float32:
+        raise NotSupported(f"float32 scale_a only, got {sa.dtype}")
+    same_device(a_q.device, scale_a=sa)
+    out = torch.empty((M, N // 2), dtype=torch.bfloat16, device=a_q.device)
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    status = _lib.lib().i8l_w8a8_mm_silu_mul(
+        a_q.data_ptr(), a_q.stride(0) if M > 1 else K, b_q.data_ptr(), b_q.stride(0),
+        b_q.stride(1), sa.data_ptr(), sa.numel(), sb.data_ptr(), sb.numel(),
+        bias.data_ptr() if bias is not None else None, bias_code, out.data_ptr(),
+        out.stride(0), int(bool(round_silu)), M, N, K, cfg, _lib.stream_of(a_q))
+    _lib.check(status, NotSupported)
+    return out
+
+
+def w8a8_mm_silu_mul_supported(m: int, n: int, k: int, config=None) -> bool:
+    """Whether w8a8_mm_silu_mul takes M tokens into an [N, K] gate_up weight."""
+    from int8_linear.kernel import Config, _cconfig
+    cfg = _cconfig(config) if isinstance(config, Config) else None
+    return _lib.lib().i8l_w8a8_mm_silu_mul_supported(m, n, k, cfg) == _lib.OK
 
 
 # Numerics the custom ops use (reference fused_quant.py:127-129 defaults);

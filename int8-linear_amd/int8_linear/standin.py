@@ -19,8 +19,9 @@ fused_quant.QUANT_MM_MAX_M tokens, the quantizer and o_proj are one kernel
 (fused_quant.quant_mm), and for the few tokens fused_quant.silu_mul_quant_mm takes,
 SiLU-and-mul+quant and down_proj are one kernel too, and up to
 fused_quant.NORM_MM_FOLD_M tokens each add+RMSNorm+quant is folded into the projection
-after it (fused_quant.add_rmsnorm_quant_mm); each gives the same bits as the two kernels it
-replaces: 4 kernels a layer at 1 token.
+after it (fused_quant.add_rmsnorm_quant_mm), and at 2-3 tokens gate_up_proj writes
+silu(gate) * up itself (fused_quant.w8a8_mm_silu_mul) for down_proj to quantize; each gives
+the same bits as the kernels it replaces: 4 kernels a layer at 1-3 tokens.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
@@ -60,10 +61,14 @@ class DecoderStandIn:
         self.configs: dict = {}
         # the same for the norm-folded linears ({name: Config}, else the library's choice)
         self.norm_configs: dict = {}
+        # and for gate_up_proj with the SiLU-and-mul epilogue
+        self.silu_configs: dict = {}
         # fold silu_mul_quant into down_proj where the library takes it (fused_down)
         self.use_fused_down = True
         # fold add_rmsnorm_quant into qkv_proj and gate_up_proj where the library takes it
         self.use_fused_norm = True
+        # the SiLU-and-mul in gate_up_proj's epilogue (and the quantizer into down_proj)
+        self.use_fused_silu = True
         self.x = torch.randn((m, HIDDEN), generator=g, device=generator_device).to(
             torch.bfloat16).to(dev)
         self.norm = torch.ones(HIDDEN, dtype=torch.bfloat16, device=dev)
@@ -106,6 +111,13 @@ class DecoderStandIn:
             fq.add_rmsnorm_quant_mm_supported(self.m, SHAPES[name][1], HIDDEN)
             for name in ("qkv_proj", "gate_up_proj"))
 
+    @property
+    def fused_silu(self) -> bool:
+        """Whether gate_up_proj writes silu(gate) * up itself (w8a8_mm_silu_mul, or with the
+        norm folded in too), so that down_proj only quantizes it; for few tokens."""
+        return self.use_fused_silu and fq.SILU_EPI_MIN_M <= self.m <= fq.SILU_EPI_MAX_M and \
+            fq.w8a8_mm_silu_mul_supported(self.m, 2 * INTER, HIDDEN)
+
     def weight_bytes(self) -> int:
         return sum(w.numel() + 4 * s.numel() for layer in self.layers for w, s in layer.values())
 
@@ -113,16 +125,21 @@ class DecoderStandIn:
         w, ws = layer[name]
         return w8a8_mm(q, w.t(), s, ws, torch.bfloat16, config=self.configs.get(name))
 
-    def norm_mm(self, layer, name: str, x: torch.Tensor, res: torch.Tensor | None):
-        """add_rmsnorm_quant then the linear, as one kernel: (output, residual_out)."""
+    def norm_mm(self, layer, name: str, x: torch.Tensor, res: torch.Tensor | None,
+                silu: bool = False):
+        """add_rmsnorm_quant then the linear, as one kernel: (output, residual_out); with
+        silu, the output is gate_up's silu(gate) * up."""
         w, ws = layer[name]
         return fq.add_rmsnorm_quant_mm(x, res, self.norm, EPS, w.t(), ws, torch.bfloat16, None,
-                                       fq.PRECISE_DIV, config=self.norm_configs.get(name))
+                                       fq.PRECISE_DIV, config=self.norm_configs.get(name),
+                                       silu_mul=silu, round_silu=fq.ROUND_SILU)
 
     def forward(self, with_residual: bool = False):
         """One step through every layer; returns the last down_proj output [m, HIDDEN] (and
         the residual stream entering the last layer's MLP norm, with_residual=True)."""
         fused_o, fused_down, fused_norm = self.fused_o, self.fused_down, self.fused_norm
+        fused_silu = self.fused_silu
+        quant_down = fused_silu and fq.quant_mm_supported(self.m, HIDDEN, INTER)
         res = self.x
         if not fused_norm:
             q, s, _ = fq.add_rmsnorm_quant(self.x, None, self.norm, EPS, fq.PRECISE_DIV)
@@ -142,11 +159,23 @@ class DecoderStandIn:
                 q, s = fq.quant_per_token(a[:, :Q_COLS], fq.PRECISE_DIV)
                 h = self.mm(layer, "o_proj", q, s)
             if fused_norm:
-                gu, res = self.norm_mm(layer, "gate_up_proj", h, res)
+                gu, res = self.norm_mm(layer, "gate_up_proj", h, res, silu=fused_silu)
             else:
                 q, s, res = fq.add_rmsnorm_quant(h, res, self.norm, EPS, fq.PRECISE_DIV)
-                gu = self.mm(layer, "gate_up_proj", q, s)
-            if fused_down:
+                if fused_silu:
+                    w, ws = layer["gate_up_proj"]
+                    gu = fq.w8a8_mm_silu_mul(q, w.t(), s, ws, fq.ROUND_SILU,
+                                             config=self.silu_configs.get("gate_up_proj"))
+                else:
+                    gu = self.mm(layer, "gate_up_proj", q, s)
+            if fused_silu:   # gu holds silu(gate) * up: quantize it into down_proj
+                w, ws = layer["down_proj"]
+                if quant_down:
+                    h = fq.quant_mm(gu, w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV)
+                else:
+                    q, s = fq.quant_per_token(gu, fq.PRECISE_DIV)
+                    h = self.mm(layer, "down_proj", q, s)
+            elif fused_down:
                 w, ws = layer["down_proj"]
                 h = fq.silu_mul_quant_mm(gu, w.t(), ws, torch.bfloat16, None, fq.PRECISE_DIV,
                                          fq.ROUND_SILU)

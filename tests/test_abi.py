@@ -265,7 +265,8 @@ def test_dynamic_quant_entry_validates_on_the_host():
     L = _lib.lib()
     assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, None) == _lib.OK
     assert L.i8l_w8a8_mm_dynq_supported(1, 4096, 4096, None) == _lib.OK
-    assert L.i8l_w8a8_mm_dynq_supported(4, 2048, 6144, None) == _lib.UNSUPPORTED
+    assert L.i8l_w8a8_mm_dynq_supported(4, 2048, 6144, None) == _lib.OK      # 12 waves of 512
+    assert L.i8l_w8a8_mm_dynq_supported(4, 2048, 3072, None) == _lib.UNSUPPORTED
     assert "one step" in _lib.last_error()
     c = _lib.CConfig(16, 32, 128, 16, 3, 1)
     assert L.i8l_w8a8_mm_dynq_supported(16, 2048, 2048, ctypes.byref(c)) == _lib.OK
@@ -300,17 +301,40 @@ def test_norm_quant_entry_validates_on_the_host():
     c = _lib.CConfig(16, 16, 512, 8, 4, 4)                     # four a CU: beyond the LDS
     assert L.i8l_add_rmsnorm_quant_mm_supported(4, 4096, 4096, ctypes.byref(c)) == _lib.UNSUPPORTED
     # argument errors come back before anything launches (no pointer is touched)
-    args = [None, None, None, 1e-6, _lib.BF16, 1, None, None, 1, 2048, None, 7, None, 0, None,
-            4096, _lib.BF16, None, 4, 4096, 2048, None, None]
+    args = [None, None, None, 1e-6, _lib.BF16, 1, 0, None, None, 1, 2048, None, 7, None, 0,
+            None, 4096, _lib.BF16, None, 4, 4096, 2048, None, None]
     assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG and "scale_b" in _lib.last_error()
-    args[11] = 4096
+    args[12] = 4096
     args[4] = _lib.F32                                          # fp32 activations
     assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.UNSUPPORTED
-    args[4], args[6] = _lib.BF16, 1                             # residual_out without residual
+    args[4], args[7] = _lib.BF16, 1                             # residual_out without residual
     assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG
-    args[6] = None
+    args[7] = None
     assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG   # x is NULL
     assert "required" in _lib.last_error()
+    args[0], args[2], args[6] = 16, 16, 3                       # an epilogue mode not defined
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.INVALID_ARG
+    args[6] = 1                                                 # SiLU epilogue without residual
+    assert L.i8l_add_rmsnorm_quant_mm(*args) == _lib.UNSUPPORTED and "SiLU" in _lib.last_error()
+
+
+def test_silu_epilogue_entry_validates_on_the_host():
+    L = _lib.lib()
+    assert L.i8l_w8a8_mm_silu_mul_supported(8, 12288, 2048, None) == _lib.OK
+    assert L.i8l_w8a8_mm_silu_mul_supported(16, 28672, 4096, None) == _lib.OK
+    assert L.i8l_w8a8_mm_silu_mul_supported(17, 12288, 2048, None) == _lib.UNSUPPORTED
+    c = _lib.CConfig(16, 32, 128, 16, 4, 1)                      # two fragments: not taken
+    assert L.i8l_w8a8_mm_silu_mul_supported(4, 12288, 2048, ctypes.byref(c)) == _lib.UNSUPPORTED
+    c = _lib.CConfig(16, 8, 512, 4, 4, 4)
+    assert L.i8l_w8a8_mm_silu_mul_supported(4, 12288, 2048, ctypes.byref(c)) == _lib.OK
+    # argument errors come back before anything launches (no pointer is touched)
+    args = [None, 2048, None, 1, 2048, None, 4, None, 1, None, 0, None, 6144, 0, 4, 12288,
+            2048, None, None]                                   # per-tensor scale_b
+    assert L.i8l_w8a8_mm_silu_mul(*args) == _lib.INVALID_ARG
+    args[8], args[10] = 12288, _lib.F32                         # an fp32 bias
+    assert L.i8l_w8a8_mm_silu_mul(*args) == _lib.UNSUPPORTED
+    args[10], args[14], args[6] = 0, 0, 1                       # M == 0: nothing to do
+    assert L.i8l_w8a8_mm_silu_mul(*args) == _lib.OK
 
 
 def test_situ_tune_writes_only_kept_sets_as_table_rows():

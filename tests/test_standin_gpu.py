@@ -108,16 +108,22 @@ def test_standin_graph_replay_equals_eager():
         assert not torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("m", [1, 3, 4])
-def test_folded_norm_gives_the_same_step(m):
-    """Up to NORM_MM_FOLD_M tokens the stand-in folds each add+RMSNorm+quant into the
-    projection after it (4 kernels a layer at one token); the step's output and residual
-    stream are the same bits with the fold and without it."""
-    say(f"standin norm fold m={m}")
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("round_silu", [False, True])
+def test_folded_kernels_give_the_same_step(m, round_silu, monkeypatch):
+    """For few tokens the stand-in folds each add+RMSNorm+quant into the projection after it,
+    the q-column quantizer into o_proj, and SiLU-and-mul+quant into down_proj or gate_up_proj's
+    epilogue (4 kernels a layer at 1-3 tokens); the step's output and residual stream are the
+    same bits with every fold and with none."""
+    say(f"standin folds m={m} round_silu={round_silu}")
+    monkeypatch.setattr(fq, "ROUND_SILU", round_silu)
     stack = DecoderStandIn(m, layers=3, seed=40 + m)
     assert stack.fused_norm == (m <= fq.NORM_MM_FOLD_M)
+    assert stack.fused_silu == (fq.SILU_EPI_MIN_M <= m <= fq.SILU_EPI_MAX_M)
     h, res = stack.forward(with_residual=True)
-    stack.use_fused_norm = False
+    stack.use_fused_norm = stack.use_fused_silu = stack.use_fused_down = False
+    monkeypatch.setattr(fq, "QUANT_MM_MAX_M", 0)
+    assert not (stack.fused_norm or stack.fused_silu or stack.fused_down or stack.fused_o)
     h0, r0 = stack.forward(with_residual=True)
     torch.cuda.synchronize()
     assert torch.equal(h, h0) and torch.equal(res, r0)
