@@ -516,13 +516,18 @@ def main() -> int:
                     help="only the config-0 roofline launches (and a copy of known size), for "
                          "rocprofv3 kernel-trace and counter runs")
     ap.add_argument("--only", choices=["quant", "prefill", "standin", "launch", "llama_decode",
-                                       "floors", "linear"],
+                                       "floors", "linear", "decode_points"],
                     default=None,
                     help="run one extra section alone (for profiling) and print its JSON")
     ap.add_argument("--calibrate", action="store_true",
                     help="with --only: also run three 256 MiB device copies (counter scale)")
     ap.add_argument("--prefill-m", type=int, nargs="+", default=None,
                     help="with --only prefill: the token counts to run (default 512-4096)")
+    ap.add_argument("--quant-m", type=int, nargs="+", default=None,
+                    help="with --only quant: the token counts to run (default 1-4096)")
+    ap.add_argument("--mark", action="store_true",
+                    help="launch a one-element marker kernel just before and just after the "
+                         "timed sweep steps, so a kernel trace shows where they lie")
     ap.add_argument("--details", default=None,
                     help="also write the result with every per-point table to this JSON file")
     ap.add_argument("--kn", default=None, help="with --only linear: K x N of the weight")
@@ -530,7 +535,15 @@ def main() -> int:
     ap.add_argument("--config", default=None,
                     help="with --only linear: bm,bn,bk,warps,stages,group_m (default: the "
                          "library's choice)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("SWEEP_CSV", "POINTS_CSV"),
+                    default=None,
+                    help="summarize two rocprofv3 kernel traces (the sweep run with --mark, "
+                         "--only decode_points --mark) into in-graph against alone kernel "
+                         "times per point, on the host (no GPU); --steps as in the sweep run")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(json.dumps({"trace_summary": trace_summary(*args.trace_summary, args.steps)}))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has "
               "one MI355X); run with --gpus 1", file=sys.stderr)
@@ -549,10 +562,12 @@ def main() -> int:
         print(json.dumps({"roofline": rf, "calibration": cal}), flush=True)
         return 0
     if args.only:
-        fn = {"quant": bench_quant, "prefill": lambda d: bench_prefill(d, args.prefill_m),
+        fn = {"quant": lambda d: bench_quant(d, args.quant_m),
+              "prefill": lambda d: bench_prefill(d, args.prefill_m),
               "standin": bench_standin, "launch": bench_launch,
               "llama_decode": bench_llama_decode, "floors": bench_floors,
-              "linear": lambda d: run_linear(d, args.kn, args.m, args.config)}[args.only]
+              "linear": lambda d: run_linear(d, args.kn, args.m, args.config),
+              "decode_points": lambda d: decode_points(d, mark=args.mark)}[args.only]
         res = {args.only: fn(dev)}
         if args.calibrate:
             res["calibration"] = copy_calibration(dev)
@@ -596,12 +611,17 @@ def main() -> int:
         graphs.append(g)
     for i in range(args.warmup):
         graphs[i % 2].replay()
+    mark = torch.zeros(1, dtype=torch.int16, device=dev)   # its add is the trace's marker
     torch.cuda.synchronize()
+    if args.mark:
+        mark.add_(1)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(args.steps):
         graphs[i % 2].replay()
     stop.record()
+    if args.mark:
+        mark.add_(1)
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(stop) / args.steps
     n_calls = len(sw.points)
@@ -629,14 +649,8 @@ def main() -> int:
         f"{result['roofline']['achieved']:.0f} GB/s ({result['roofline']['frac']:.1%})")
 
     if not args.no_extra:
-        table = []
-        for i, (label, m, k, n, bias, d) in enumerate(sw.points):
-            us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies[(k, n)], windows=3)
-            gbs = gemm_bytes(m, k, n, bias) / (us * 1e-6) / 1e9
-            table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
-        details["decode_points"] = {"cols": ["shape", "M", "bias", "us", "hbm_frac"],
-                                    "rows": table}
-        result["decode"] = summary_decode(table)
+        details["decode_points"] = decode_points(dev, sw)
+        result["decode"] = summary_decode(details["decode_points"]["rows"])
         for name, fn in (("quant", bench_quant), ("llama_decode", bench_llama_decode),
                          ("prefill", bench_prefill), ("standin", bench_standin),
                          ("launch", bench_launch), ("floors", bench_floors)):
@@ -729,7 +743,92 @@ SUMMARIES = {"quant": summary_quant, "llama_decode": summary_llama, "prefill": s
              "standin": summary_standin, "launch": lambda _: None, "floors": summary_floors}
 
 
-def bench_quant(dev) -> dict:
+def trace_summary(sweep_csv: str, points_csv: str, steps: int) -> dict:
+    """In-graph against alone, per decode-sweep point, from two rocprofv3 kernel traces (CSV):
+    the sweep run with --mark (the timed steps lie between two marker dispatches, each step
+    the 72 points in order, a split of K being two dispatches) and --only decode_points --mark
+    (each point's own graph replays after a marker dispatch).  Kernel durations are the
+    trace's end - start of each dispatch: in the graph, the mean over the timed steps; alone,
+    the median over the point's replays."""
+    import csv
+
+    from int8_linear.shapes import SHAPES
+
+    def dispatches(path):
+        rows = list(csv.DictReader(open(path)))
+        rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+        return [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                for r in rows]
+
+    def is_mark(name):     # the in-place add on the one-element int16 marker tensor
+        return "elementwise" in name and "add" in name.lower() and "short" in name
+
+    def short(name):
+        return name.split("(")[0].replace("void ", "").replace("i8l::", "")
+
+    labels = [(lbl, m, b) for lbl, k, n in SHAPES["qwen3-1.7b-vllm"] for m in DECODE_M
+              for b in (0, 1)]
+    sw = dispatches(sweep_csv)
+    marks = [i for i, (nm, _) in enumerate(sw) if is_mark(nm)]
+    inner = sw[marks[-2] + 1: marks[-1]]
+    per_step = len(inner) // steps
+    if per_step * steps != len(inner):
+        raise SystemExit(f"{len(inner)} dispatches between the marks do not make {steps} steps")
+    in_graph = []   # per point: (kernel names, summed mean us)
+    pos = 0
+    step0 = inner[:per_step]
+    for _ in labels:
+        names, idx = [short(step0[pos][0])], [pos]
+        pos += 1
+        if pos < per_step and "splitk_sum" in step0[pos][0]:
+            names.append(short(step0[pos][0]))
+            idx.append(pos)
+            pos += 1
+        us = sum(statistics.mean(inner[s * per_step + i][1] for s in range(steps)) for i in idx)
+        in_graph.append((" + ".join(names), us))
+    if pos != per_step:
+        raise SystemExit(f"the step's {per_step} dispatches do not map onto {len(labels)} points")
+    pt = dispatches(points_csv)
+    pmarks = [i for i, (nm, _) in enumerate(pt) if is_mark(nm)] + [len(pt)]
+    alone = []
+    for a, b in zip(pmarks[:-1], pmarks[1:]):
+        seg = [d for d in pt[a + 1: b] if "splitk_sum" not in d[0]]
+        sk = [d for d in pt[a + 1: b] if "splitk_sum" in d[0]]
+        us = statistics.median(d[1] for d in seg) + (statistics.median(d[1] for d in sk) if sk else 0)
+        alone.append(us)
+    if len(alone) != len(labels):
+        raise SystemExit(f"{len(alone)} marked segments for {len(labels)} points")
+    rows = [[lbl, m, b, names, round(g, 3), round(al, 3), round(g - al, 3)]
+            for (lbl, m, b), (names, g), al in zip(labels, in_graph, alone)]
+    return {"cols": ["shape", "M", "bias", "kernel", "in_graph_us", "alone_us", "diff_us"],
+            "rows": rows, "mean_in_graph_us": round(statistics.mean(r[4] for r in rows), 3),
+            "mean_alone_us": round(statistics.mean(r[5] for r in rows), 3)}
+
+
+def decode_points(dev, sw=None, mark: bool = False) -> dict:
+    """Each point of the decode sweep timed on its own: a HIP graph of back-to-back calls of
+    that point alone, its weight rotating through the shape's copies (checked first when the
+    sweep is built here)."""
+    import torch
+    if sw is None:
+        from int8_linear.shapes import SHAPES
+        sw = Sweep(SHAPES["qwen3-1.7b-vllm"], DECODE_M, dev)
+        for i, (label, m, k, n, bias, d) in enumerate(sw.points):
+            out = checked_mm(d)
+            if not check_linear(out, d) <= 1e-2 or not torch.equal(sw.call(i, 0), out):
+                raise SystemExit(f"FAIL: {label} M={m} bias={bias}")
+    table = []
+    marker = torch.zeros(1, dtype=torch.int16, device=dev)
+    for i, (label, m, k, n, bias, d) in enumerate(sw.points):
+        if mark:                 # one dispatch before each point's launches, for a trace
+            marker.add_(1)
+        us = graph_time_us(lambda j, i=i: sw.call(i, j), 2 * sw.copies[(k, n)], windows=3)
+        gbs = gemm_bytes(m, k, n, bias) / (us * 1e-6) / 1e9
+        table.append([label, m, int(bias), round(us, 2), round(gbs / HBM_PEAK_GBS, 3)])
+    return {"cols": ["shape", "M", "bias", "us", "hbm_frac"], "rows": table}
+
+
+def bench_quant(dev, ms=None) -> dict:
     """the two fused quantizers at H=2048 / I=6144.  Each size is checked
     first: the C entry point writes into poisoned outputs (codes 99, NaN scales and residual),
     which are compared with the reference's CPU arithmetic (ref_norm, ref_silu)."""
@@ -744,7 +843,7 @@ def bench_quant(dev) -> dict:
         return torch.full(shape, float("nan"), device=dev,
                           dtype=torch.float32 if shape[1] == 1 else torch.bfloat16)
     rows = []
-    for m in QUANT_M:
+    for m in ms or QUANT_M:
         g = torch.Generator().manual_seed(m)
         copies = max(2, -(-ROTATE_BYTES // (m * 2048 * 7 + 1)))
         copies = min(copies, 64)
@@ -1089,9 +1188,10 @@ def bench_floors(dev) -> dict:
     (back-to-back launches in a HIP graph, HIP events on the launch stream), by the probe
     kernels of int8-linear_amd/probes/i8l_floors.hip:
       * an empty kernel at three grid shapes (the decode GEMM's is 256 x 512 threads);
-      * a read of 8 / 12 / 24 / 120 MiB (the weights of config 0, of Qwen3 down_proj and
-        gate_up, of Llama-3-8B gate_up) rotating through >= 768 MiB of buffers so every read
-        comes from HBM, and 8 MiB hot; the best of 1, 2, 4 and 8 loads a thread;
+      * a read of 4 / 8 / 12 / 16 / 24 / 120 MiB (the weights of Qwen3 o_proj, config 0,
+        Qwen3 down_proj, Llama-3-8B o_proj, Qwen3 gate_up, Llama-3-8B gate_up) rotating
+        through >= 768 MiB of buffers so every read comes from HBM, and 8 MiB hot; the best
+        of 1, 2, 4 and 8 loads a thread;
       * back-to-back int8 MFMAs on every SIMD: the rate sustained under load, on constant
         operands and on random ones (toggling data costs power, and the clock follows);
       * the rate at which CUs take in L2-resident bytes (each workgroup re-reading 64 KiB
@@ -1129,7 +1229,8 @@ def bench_floors(dev) -> dict:
         empty.append([blocks, threads, round(us, 3)])
         log(f"floor empty kernel {blocks}x{threads}: {us:.2f} us")
     reads = []
-    for mib, cold in ((8, True), (12, True), (24, True), (120, True), (8, False)):
+    for mib, cold in ((4, True), (8, True), (12, True), (16, True), (24, True), (120, True),
+                      (8, False)):
         size = mib << 20
         copies = max(2, -(-ROTATE_BYTES // size)) if cold else 1
         bufs = [torch.zeros(size, dtype=torch.uint8, device=dev) for _ in range(copies)]

@@ -25,6 +25,7 @@ LIB = HERE / "int8_linear" / "libint8_linear_amd.so"
 PROBES_SRC = HERE / "probes" / "i8l_floors.hip"
 PROBES_LIB = HERE / "probes" / "libi8l_floors.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
 
 # -ffp-contract=off: the epilogue and quantizer arithmetic is the sequence of IEEE ops
 #   written, which the CPU oracle reproduces bit for bit.
@@ -70,9 +71,6 @@ def build(verbose: bool = False) -> Path:
     if verbose:
         print(f"built {fast}", file=sys.stderr)
     return LIB
-
-
-CXX = os.environ.get("CXX", "g++")
 
 
 def _build_probes() -> Path:

@@ -162,6 +162,17 @@ __device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float
   return wave_max(p.lane < nw ? sh[p.slot * nw + p.lane] : 0.0f);
 }
 
+// clamp(rint(v), -128, 127) as the low byte of the result (the byte an int8 code is stored
+// as), without a float-to-int conversion: the clamp is taken first, which gives the same
+// integer since both bounds are integers, and adding 1.5 * 2^23 rounds it to an integer in
+// that one IEEE addition (round half to even, as rint), leaving it in the low mantissa bits
+// of a float whose exponent is fixed: bits = 0x4B400000 + rint(v), two's complement in the
+// low byte for negative codes.
+__device__ __forceinline__ uint32_t code_rne(float v) {
+  const float t = fminf(fmaxf(v, -128.0f), 127.0f) + 12582912.0f;
+  return __float_as_uint(t) & 0xffu;
+}
+
 // The quantizer of a row whose values y (J chunks of 8 per lane) are final: absmax over the
 // row, scale and reciprocal, codes stored as 8-byte pieces, the scale by the row's first lane.
 template <int J, bool VEC, bool MULTI, bool FULL = false>
@@ -187,11 +198,7 @@ __device__ __forceinline__ void quantize_store(float (&y)[J][8], const RowPos& p
     const int e0 = chunk_base<J>(p, j);
     uint32_t c[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = __builtin_rintf(y[j][i] * inv);
-      v = fminf(fmaxf(v, -128.0f), 127.0f);
-      c[i] = (uint32_t)(int)v & 0xffu;
-    }
+    for (int i = 0; i < 8; ++i) c[i] = code_rne(y[j][i] * inv);
     if (VEC) {
       if (FULL || e0 < n) {
         const uint32_t lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
@@ -350,10 +357,10 @@ silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
   // to +inf above 89, and a NaN g makes the quotient NaN whatever d is (checked for every
   // bf16 and fp16 g on gfx950).
   // a = g / d.  For -87 < g < +inf, d is in [1, 7e37], its reciprocal is normal, and one
-  // Newton-Markstein correction of g * rcp(d) gives the correctly rounded quotient, with the
-  // sign copied from g so that g = -0 gives -0 (checked against IEEE division for every
-  // bf16 and fp16 g in that range on gfx950).  A wave holding any other g recomputes its
-  // values with IEEE division.
+  // Newton-Markstein correction of g * rcp(d) gives the correctly rounded quotient (checked
+  // against IEEE division for every bf16 and fp16 g in that range on gfx950), up to the
+  // sign of a zero quotient, which no output of this kernel depends on.  A wave holding any
+  // other g recomputes its values with IEEE division.
   float y[J][8];
   float gmin = __builtin_inff(), gmax = -__builtin_inff();
 #pragma unroll
@@ -369,9 +376,10 @@ silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
         const float r0 = __builtin_amdgcn_rcpf(d);
         const float q0 = g[h] * r0;
         const float e = __builtin_fmaf(-d, q0, g[h]);
-        const float q1 = __builtin_fmaf(e, r0, q0);
-        a[h] = __uint_as_float((__float_as_uint(q1) & 0x7fffffffu) |
-                               (__float_as_uint(g[h]) & 0x80000000u));
+        // the quotient's sign is g's except for g = -0, where the correction gives +0 for
+        // the IEEE -0; the sign of a zero reaches no output (its code is 0 either way, and
+        // absmax takes |y|), so it is not restored here
+        a[h] = __builtin_fmaf(e, r0, q0);
         gmin = fminf(gmin, g[h]);
         gmax = fmaxf(gmax, g[h]);
       }
@@ -419,6 +427,7 @@ quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q
 }
 
 bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 
 int next_pow2(int v) {
   int p = 1;
@@ -644,8 +653,8 @@ extern "C" int i8l_silu_mul_quant(const void* gate_up, int8_t* q, float* scale, 
   if (M == 0) return I8L_OK;
   const int i = (int)I;
   const bool vec = i % 8 == 0 && a16(gate_up) && a16(q);
-  const Geom g = silu_geom(M, i, vec);
   const hipStream_t st = (hipStream_t)stream;
+  const Geom g = silu_geom(M, i, vec);
   auto go = [&](auto launch) {
     launch(g, vec, grid_of(M, g), st, (const uint16_t*)gate_up, q, scale, M, i, precise_div);
   };

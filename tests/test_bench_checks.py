@@ -100,3 +100,46 @@ def test_result_sections_are_scalars():
         json.dumps(out)
     assert bench.summary_prefill(prefill)["qkv_m4096_frac"] == 0.4
     assert bench.summary_standin(standin)["m1_us_per_layer"] == 25.0
+
+
+def test_trace_summary_maps_dispatches_onto_sweep_points(tmp_path):
+    """bench.py --trace-summary on synthetic kernel traces shaped as the two runs make them:
+    the timed steps between marker dispatches (a split of K being two dispatches), and each
+    point's replays after its own marker."""
+    import csv as csvmod
+
+    n_points = 4 * len(bench.DECODE_M) * 2
+    split = {5, 40}                                  # points launched as two kernels
+    head = ["Kernel_Name", "Start_Timestamp", "End_Timestamp"]
+
+    def write(path, events):
+        t = 0
+        with open(path, "w", newline="") as f:
+            w = csvmod.writer(f)
+            w.writerow(head)
+            for name, dur in events:
+                w.writerow([name, t, t + int(dur * 1000)])
+                t += int(dur * 1000) + 500
+
+    mark = ("void at::native::vectorized_elementwise_kernel<4, CUDAFunctorOnSelf_add<short>>()", 1)
+    step = []
+    for p in range(n_points):
+        step.append((f"void i8l::gemm_k{p}(int)", 2.0 + p / 100))
+        if p in split:
+            step.append(("void i8l::splitk_sum<2>(int)", 1.0))
+    steps = 3
+    write(tmp_path / "sweep.csv", [("void warm()", 5)] + [mark] + step * steps + [mark] + step)
+    pts = [("void check()", 3)]
+    for p in range(n_points):
+        pts.append(mark)
+        for _ in range(5):
+            pts.append((f"void i8l::gemm_k{p}(int)", 1.5 + p / 100))
+            if p in split:
+                pts.append(("void i8l::splitk_sum<2>(int)", 0.5))
+    write(tmp_path / "points.csv", pts)
+    out = bench.trace_summary(str(tmp_path / "sweep.csv"), str(tmp_path / "points.csv"), steps)
+    rows = out["rows"]
+    assert len(rows) == n_points
+    assert rows[5][3] == "gemm_k5 + splitk_sum<2>" and rows[5][4] == 3.05 and rows[5][5] == 2.05
+    assert rows[6][3] == "gemm_k6" and rows[6][4] == 2.06 and rows[6][5] == 1.56
+    assert all(abs(r[6] - (r[4] - r[5])) < 1e-9 for r in rows)
