@@ -39,6 +39,7 @@ scalar fields in each section; the per-point tables are printed on the lines bef
 from __future__ import annotations
 
 import argparse
+import collections
 import json
 import os
 import statistics
@@ -540,7 +541,15 @@ def main() -> int:
                     help="summarize two rocprofv3 kernel traces (the sweep run with --mark, "
                          "--only decode_points --mark) into in-graph against alone kernel "
                          "times per point, on the host (no GPU); --steps as in the sweep run")
+    ap.add_argument("--traffic-summary", nargs=4,
+                    metavar=("KIND", "FETCH_CSV", "WRITE_CSV", "RUN_JSON"), default=None,
+                    help="HBM traffic per launch (KIND config0 or prefill) from a FETCH_SIZE and "
+                         "a WRITE_SIZE counter run of the same command and that command's "
+                         "output line, on the host (no GPU)")
     args = ap.parse_args()
+    if args.traffic_summary:
+        print(json.dumps(traffic_summary(*args.traffic_summary), indent=1))
+        return 0
     if args.trace_summary:
         print(json.dumps({"trace_summary": trace_summary(*args.trace_summary, args.steps)}))
         return 0
@@ -803,6 +812,90 @@ def trace_summary(sweep_csv: str, points_csv: str, steps: int) -> dict:
     return {"cols": ["shape", "M", "bias", "kernel", "in_graph_us", "alone_us", "diff_us"],
             "rows": rows, "mean_in_graph_us": round(statistics.mean(r[4] for r in rows), 3),
             "mean_alone_us": round(statistics.mean(r[5] for r in rows), 3)}
+
+
+PREFILL_SHAPES = {"qkv_proj": (4096, 6144), "o_proj": (4096, 4096),
+                  "gate_up_proj": (4096, 28672), "down_proj": (14336, 4096)}
+
+
+def traffic_summary(kind: str, fetch_csv: str, write_csv: str, run_json: str) -> dict:
+    """HBM bytes per launch from two rocprofv3 counter runs (CSV) of the same command, one with
+    FETCH_SIZE and one with WRITE_SIZE (KiB a dispatch): kind "config0" for `--roofline-only`,
+    "prefill" for `--only prefill --prefill-m 4096 --calibrate`; `run_json` is that command's
+    last stdout line (the configs it ran).  Each counter is scaled by what it reads for the
+    run's 256 MiB device copies (the largest copy dispatches); the GEMM dispatches (the
+    library's kernels, in order) fall into one group per shape, where the kernel or its grid
+    changes, and each group's mean per dispatch is its launch's traffic."""
+    import csv
+
+    def load(path):
+        val, meta = collections.defaultdict(float), {}
+        for r in csv.DictReader(open(path)):
+            d = int(r["Dispatch_Id"])
+            val[d] += float(r["Counter_Value"])
+            meta[d] = (r["Kernel_Name"], int(r["Grid_Size"]))
+        ds = sorted(val)
+        # the calibration copies are the largest copy dispatches (other copies, e.g. of the
+        # rotating weight buffers, may share their kernel and grid)
+        copies = [val[d] for d in ds if "copyBuffer" in meta[d][0]]
+        top = max(copies, default=0.0)
+        copy = statistics.mean(v for v in copies if v >= 0.99 * top) if copies else 0.0
+        groups, prev = [], None
+        for d in ds:
+            if "i8l::" not in meta[d][0] or "gemm" not in meta[d][0]:
+                continue
+            if meta[d] != prev:
+                groups.append([])
+                prev = meta[d]
+            groups[-1].append(val[d])
+        return [statistics.mean(g) for g in groups], copy, [meta[d][0] for d in ds]
+
+    fetch, fcopy, _ = load(fetch_csv)
+    write, wcopy, _ = load(write_csv)
+    if not fcopy or not wcopy:
+        raise SystemExit("no device copy in the runs: add --calibrate")
+    cmd = {"config0": "--roofline-only", "prefill": "--only prefill --prefill-m 4096 --calibrate"}[kind]
+    commands = [f"rocprofv3 --pmc {c} --output-format csv -d DIR/{c} -o c -- python3 bench.py "
+                f"{cmd} > DIR/{c}.out" for c in ("FETCH_SIZE", "WRITE_SIZE")]
+    commands.append(f"python3 bench.py --traffic-summary {kind} "
+                    "DIR/FETCH_SIZE/c_counter_collection.csv "
+                    "DIR/WRITE_SIZE/c_counter_collection.csv DIR/FETCH_SIZE.out")
+    copy_bytes = 256 << 20
+    fs, ws = copy_bytes / (fcopy * 1024), copy_bytes / (wcopy * 1024)
+    run = json.loads(open(run_json).read().strip().splitlines()[-1])
+    cal = {"copy_bytes": copy_bytes, "fetch_kib": round(fcopy, 2), "write_kib": round(wcopy, 2),
+           "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+    note = ("FETCH_SIZE counts bytes the L2 fetches from the fabric (Infinity Cache or HBM), so "
+            "these are an upper bound on HBM bytes")
+
+    def record(f, w, algorithmic):
+        return {"fetch_kib_per_launch": round(f, 2), "write_kib_per_launch": round(w, 2),
+                "bytes_per_launch": int(round(f * 1024 * fs + w * 1024 * ws)),
+                "algorithmic_bytes_per_launch": algorithmic}
+
+    if kind == "config0":
+        if len(fetch) != 1 or len(write) != 1:
+            raise SystemExit(f"expected one GEMM launch group, found {len(fetch)} / {len(write)}")
+        rf = run["roofline"]
+        out = {"config": rf["kernel"].split("config ")[1].split(" (")[0],
+               "workload": "BASELINE config 0 (M=16, K=2048, N=4096, no bias, bf16 out), cold "
+                           "weights", "copy_calibration": cal, "note": note,
+               "commands": commands}
+        out.update(record(fetch[0], write[0], rf["bytes_per_launch"]))
+        return out
+    per = run["prefill"]["per_shape"]
+    if len(fetch) != len(PREFILL_SHAPES) or len(write) != len(PREFILL_SHAPES):
+        raise SystemExit(f"expected {len(PREFILL_SHAPES)} GEMM launch groups, found "
+                         f"{len(fetch)} / {len(write)}")
+    out = {"workload": "BASELINE config 3 at M=4096 (Llama-3-8B shapes, bench.py --only "
+                       "prefill --prefill-m 4096)", "copy_calibration": cal, "note": note,
+           "commands": commands, "shapes": {}}
+    m = 4096
+    for i, (lbl, (k, n)) in enumerate(PREFILL_SHAPES.items()):
+        rec = {"config": per[lbl]["kernel"].split("config ")[1].split(" (")[0]}
+        rec.update(record(fetch[i], write[i], m * k + k * n + 4 * m + 4 * n + 2 * m * n))
+        out["shapes"][lbl] = rec
+    return out
 
 
 def decode_points(dev, sw=None, mark: bool = False) -> dict:

@@ -143,3 +143,54 @@ def test_trace_summary_maps_dispatches_onto_sweep_points(tmp_path):
     assert rows[5][3] == "gemm_k5 + splitk_sum<2>" and rows[5][4] == 3.05 and rows[5][5] == 2.05
     assert rows[6][3] == "gemm_k6" and rows[6][4] == 2.06 and rows[6][5] == 1.56
     assert all(abs(r[6] - (r[4] - r[5])) < 1e-9 for r in rows)
+
+
+def test_traffic_summary_groups_launches_and_scales_by_the_copies(tmp_path):
+    """bench.py --traffic-summary on synthetic counter runs shaped as rocprofv3 writes them:
+    GEMM dispatches grouped by shape where the kernel or grid changes (o_proj and down_proj
+    share a kernel and grid, with gate_up between them), scaled by the 256 MiB copies'
+    readings, and the configs taken from the run's output line."""
+    import csv as csvmod
+
+    head = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    kernels = [("void i8l::gemm_dmap<256, 192>(int)", 98304, 90000.0, 49152.0),
+               ("void i8l::gemm_dmap<256, 256>(int)", 131072, 50000.0, 32768.0),
+               ("void i8l::gemm_dmap<256, 256>(int)", 229376, 340000.0, 229376.0),
+               ("void i8l::gemm_dmap<256, 256>(int)", 131072, 170000.0, 32768.0)]
+
+    def write(path, col, scale):
+        rows, did = [], 0
+        for name, grid, f, w in kernels:
+            for _ in range(3):                                  # a check and two timed launches
+                did += 1
+                rows.append([did, name, grid, col, (f if col == "FETCH_SIZE" else w) * scale])
+        for _ in range(3):                                      # the three calibration copies
+            did += 1
+            val = 131072.0 if col == "FETCH_SIZE" else 262144.0
+            rows.append([did, "__amd_rocclr_copyBuffer", 131072, col, val])
+        for _ in range(5):                                      # small copies, same grid
+            did += 1
+            rows.append([did, "__amd_rocclr_copyBuffer", 131072, col, 4096.0])
+        with open(path, "w", newline="") as fh:
+            wr = csvmod.writer(fh)
+            wr.writerow(head)
+            wr.writerows(rows)
+
+    write(tmp_path / "f.csv", "FETCH_SIZE", 1.0)
+    write(tmp_path / "w.csv", "WRITE_SIZE", 1.0)
+    cfgs = ["256x192x128 w8 s10 g4", "256x256x128 w8 s10 g8", "256x256x128 w8 s10 g4",
+            "256x256x128 w8 s10 g4"]
+    run = {"prefill": {"per_shape": {lbl: {"kernel": f"gemm_dmap, config {c} (x)"}
+                                     for lbl, c in zip(bench.PREFILL_SHAPES, cfgs)}}}
+    (tmp_path / "run.out").write_text("log line\n" + json.dumps(run) + "\n")
+    out = bench.traffic_summary("prefill", str(tmp_path / "f.csv"), str(tmp_path / "w.csv"),
+                                str(tmp_path / "run.out"))
+    assert out["copy_calibration"]["fetch_scale"] == 2.0
+    assert out["copy_calibration"]["write_scale"] == 1.0
+    sh = out["shapes"]
+    assert list(sh) == list(bench.PREFILL_SHAPES)
+    assert sh["o_proj"]["config"] == cfgs[1] and sh["down_proj"]["config"] == cfgs[3]
+    assert sh["gate_up_proj"]["bytes_per_launch"] == 340000 * 1024 * 2 + 229376 * 1024
+    assert sh["down_proj"]["fetch_kib_per_launch"] == 170000.0
+    m, k, n = 4096, 4096, 6144
+    assert sh["qkv_proj"]["algorithmic_bytes_per_launch"] == m * k + k * n + 4 * m + 4 * n + 2 * m * n
