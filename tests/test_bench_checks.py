@@ -75,6 +75,16 @@ def test_quantizer_check_rejects_planted_mistakes():
         bench.check_quant(many, s, q0, s0, "1600 codes off by one")
     with pytest.raises(SystemExit):
         bench.check_quant(q, s * (1 + 1e-4), q0, s0, "scales off")
+    one = s.clone()
+    one[5] = one[5] * (1 + 2.0 ** -8)                     # one row a bf16 step of absmax away
+    bench.check_quant(q, one, q0, s0, "one row's scale a bf16 step away")
+    one[5] = s[5] * (1 + 2.0 ** -5)                       # too far
+    with pytest.raises(SystemExit):
+        bench.check_quant(q, one, q0, s0, "one row's scale far off")
+    two = s.clone()
+    two[1:3] = two[1:3] * (1 + 2.0 ** -8)                 # two of 16 rows: more than allowed
+    with pytest.raises(SystemExit):
+        bench.check_quant(q, two, q0, s0, "two rows' scales off")
     with pytest.raises(SystemExit):
         bench.check_quant(q, torch.full_like(s, float("nan")), q0, s0, "scales never written")
 
