@@ -316,6 +316,16 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 
 typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 
+// Workgroup barrier for data the waves exchange through LDS stores (ds_write): each wave's
+// LDS operations have completed (lgkmcnt 0), then s_barrier.  Unlike __syncthreads() it does
+// not wait for the wave's outstanding global loads and direct-to-LDS copies (vmcnt), so a
+// weight copy requested before it stays in flight across it; it does not publish
+// direct-to-LDS data to other waves (each wave waits for its own copies).
+__device__ __forceinline__ void lds_sync() {
+  wait_lgkmcnt0();
+  lds_barrier();
+}
+
 // ------------------------------------------------------------------ host helpers
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 

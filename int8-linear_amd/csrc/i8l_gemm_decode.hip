@@ -700,7 +700,7 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int f = 0; f < NF; ++f) red[(wave * FR + i * NF + f) * 64 + lane] = acc[i][f];
-    __syncthreads();
+    lds_sync();
     if (wave < FR) {
       v4i sum = red[wave * 64 + lane];
 #pragma unroll
@@ -714,7 +714,7 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
         if (mrow < e.M && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sam);
       }
     }
-    __syncthreads();  // the partials of the next tile overwrite the reduction area
+    lds_sync();  // the partials of the next tile overwrite the reduction area
   }
 }
 
@@ -861,7 +861,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
     am = group_max<CH>(am);
     if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
   }
-  __syncthreads();
+  lds_sync();
   auto row_scale = [&](int r, float& scale, float& inv) {
     float absmax = rmax[r];
 #pragma unroll

@@ -159,7 +159,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
     const double node = group_tree_sum<CH>(s[0]);
     if (cchunk == 0) dsum[wave * 16 + r] = node;
   }
-  __syncthreads();
+  lds_sync();
 
   // the row's sum over the waves' nodes, rsqrt, y = cast(f32(cast(x * rs)) * gamma), and the
   // row's absmax
@@ -192,7 +192,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
     am = group_max<CH>(am);
     if (cchunk == 0) rmax[wave * 16 + r] = am;
   }
-  __syncthreads();
+  lds_sync();
 
   // scale and codes (the quantizer of add_rmsnorm_quant_kernel), codes into the code tile
 #pragma unroll
@@ -269,7 +269,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
         acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s], acc[f], 0, 0, 0);
 #pragma unroll
     for (int f = 0; f < NF; ++f) red[(wave * NF + f) * 64 + lane] = acc[f];
-    __syncthreads();
+    lds_sync();
     if (wave < NF) {
       v4i sum = red[wave * 64 + lane];
 #pragma unroll
@@ -283,7 +283,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
         if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, r16, ncol, sum, cl, sam);
       }
     }
-    __syncthreads();  // the partials of the next tile overwrite the reduction area
+    lds_sync();  // the partials of the next tile overwrite the reduction area
   }
 }
 
@@ -316,16 +316,19 @@ bool nq_ok(const i8l_config& c, int64_t K) {
 }
 
 // The untuned choice, from a sweep of the built tiles on MI355X (K = 2048, N = 4096 and
-// 12288, 1-8 tokens, HIP graph, cold weights): one token takes 4 waves of 512-byte slices
-// (the fewest passes of the shortest prologue), more tokens 8 waves of 256-byte slices
-// (the row work spread over twice the lanes); 16 columns a tile (8 when N does not give 256
+// 12288, 1-4 tokens, HIP graph, cold weights): 4 waves of 512-byte slices (the fewest passes
+// of the shortest prologue) for one token, and up to 3 tokens where every workgroup has one
+// tile (N = 4096 at 2 / 3 tokens: 4.25 / 5.85 us against 4.80 / 6.15 with 8 waves); otherwise
+// 8 waves of 256-byte slices (the row work spread over twice the lanes, N = 12288 at 2 / 3
+// tokens: 6.48 / 8.29 us against 6.61 / 8.80); 16 columns a tile (8 when N does not give 256
 // tiles of 16); two workgroups a compute unit where a workgroup would otherwise walk more
 // than one tile and the LDS holds two.  K = 4096 takes 8 waves of 512 bytes.
 bool default_nq_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   const int nc = N % 16 == 0 && N / 16 >= 256 ? 16 : 8;
   static const int one[3][2] = {{512, 4}, {256, 8}, {512, 8}};    // (bk, waves) by preference
   static const int more[3][2] = {{256, 8}, {512, 4}, {512, 8}};
-  const int (&pref)[3][2] = M <= 1 ? one : more;
+  const bool one_tile = N / nc <= cu_count();
+  const int (&pref)[3][2] = M <= 1 || (M <= 3 && one_tile) ? one : more;
   for (const auto& bw : pref)
     for (int g : {2, 1}) {
       if (g == 2 && N / nc <= 256) continue;

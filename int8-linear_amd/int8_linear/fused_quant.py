@@ -267,12 +267,13 @@ def silu_mul_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 # Largest M that add_rmsnorm_quant_mm takes (the kernel's limit): every workgroup normalizes
 # and quantizes the token rows itself, while its first weight tile is in flight.
 NORM_MM_MAX_M = 8
-# Largest M for which the decoder stand-in folds the norm into its projections.  The row work
-# every workgroup repeats is ~0.24 us of VALU a token row on each compute unit, so the fold
-# pays only for few tokens: measured on MI355X (HIP graph, cold weights, K = 2048), one launch
-# against add_rmsnorm_quant + w8a8_mm at N = 4096 is 4.41 / 4.77 / 6.02 / 8.24 us against
-# 5.92 / 6.35 / 6.42 / 6.32 us at 1 / 2 / 4 / 8 tokens, at N = 12288 6.58 / 6.68 / 8.39 /
-# 11.09 against 8.74 / 8.78 / 8.64 / 8.89 us.
+# Largest M for which the decoder stand-in folds the norm into its projections.  Every
+# workgroup repeats the row work, so the fold pays only for few tokens: measured on MI355X
+# (HIP graph, cold weights, K = 2048), one launch against add_rmsnorm_quant + w8a8_mm at
+# N = 4096 is 3.79 / 4.31 / 5.90 / 6.13 / 8.32 us against 5.98 / 6.13 / 6.38 / 6.37 / 6.39 us
+# at 1 / 2 / 3 / 4 / 8 tokens, at N = 12288 6.03 / 6.48 / 8.15 / 8.28 / 12.10 against
+# 8.59 / 8.85 / 8.84 / 9.00 / 9.09 us; in the 28-layer stand-in the folds lose from 5 tokens
+# (29.68 us a layer unfolded at 5 against 33.29 folded).
 NORM_MM_FOLD_M = 4
 
 
@@ -343,13 +344,13 @@ def add_rmsnorm_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 
 # Token counts for which the decoder stand-in computes the SiLU-and-mul in gate_up_proj's
 # epilogue and folds the quantizer into down_proj (the kernel takes up to 16 tokens).
-# Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with / without:
-# 21.63 / 21.54 at 1 token, 23.00 / 23.59 at 2, 26.33 / 26.92 at 3, 27.67 / 27.57 at 4,
-# 30.87 / 29.37 at 5, 33.00 / 30.32 at 8: the paired gate/up epilogue costs gate_up 0.6-0.8 us
-# (6.58 against 5.91 at one token), which the cheaper down_proj prologue repays only at 2-3
-# tokens, and from 5 tokens every CU repeats the quantizer of 6144 values a row.
+# Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with the norm folded
+# in, with / without: 20.35 / 20.21 at 1 token (where silu_mul_quant_mm folds the whole SiLU
+# chain into down_proj instead), 22.06 / 23.46 at 2, 26.09 / 26.90 at 3, 26.92 / 27.44 at 4;
+# from 5 tokens no fold pays (29.68 us a layer at 5 unfolded against 33.29 with the norm
+# folded and 34.69 with both): every CU repeats the row work of each folded quantizer.
 SILU_EPI_MIN_M = 2
-SILU_EPI_MAX_M = 3
+SILU_EPI_MAX_M = 4
 
 
 def w8a8_mm_silu_mul(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
