@@ -15,6 +15,7 @@ import torch
 from helpers import bits, np_, say
 from int8_linear import fused_quant as fq
 from int8_linear.kernel import Config, NotSupported, w8a8_mm
+from int8_linear.kernel import supported as kernel_supported
 from oracle import oracle as o
 
 pytestmark = pytest.mark.gpu
@@ -138,3 +139,36 @@ def test_declines_what_it_does_not_take():
         fq.add_rmsnorm_quant_mm(x, r, gamma.float(), EPS, w.t(), sb)   # weight of another dtype
     with pytest.raises(NotSupported):
         fq.add_rmsnorm_quant_mm(x, r, gamma, EPS, w.t().contiguous(), sb)   # N-contiguous weight
+
+
+@pytest.mark.parametrize("silu", [False, True])
+def test_repeated_calls_with_tiles_in_flight(silu):
+    """The cross-wave exchanges of the persistent kernel and of the fold's prologue meet at
+    barriers that do not wait for the weight copies in flight (the next tile's, or the first
+    tile's during the prologue): 40 calls in a row at shapes where every workgroup walks
+    several column tiles and two workgroups share a CU, each against the first and against the
+    two launches, and the plain persistent GEMM and the SiLU epilogue the same way."""
+    k, n = 2048, 12288
+    for m in (1, 2, 4, 8):
+        say(f"norm_mm repeated silu={silu} m={m}")
+        x, r, gamma, w, sb, _ = operands(m, k, n, 400 + m)
+        for cfg in (None, Config(16, 16, 256, 8, 4, 2), Config(16, 16, 512, 4, 4, 2)):
+            if cfg is not None and not fq.add_rmsnorm_quant_mm_supported(m, n, k, cfg):
+                continue
+            outs = [fq.add_rmsnorm_quant_mm(x, r, gamma, EPS, w.t(), sb, config=cfg,
+                                            silu_mul=silu)[0] for _ in range(40)]
+            torch.cuda.synchronize()
+            assert all(torch.equal(o.view(torch.int16), outs[0].view(torch.int16)) for o in outs)
+            q, s, _ = fq.add_rmsnorm_quant(x, r, gamma, EPS)
+            ref = (fq.w8a8_mm_silu_mul(q, w.t(), s, sb) if silu
+                   else w8a8_mm(q, w.t(), s, sb, torch.bfloat16))
+            assert torch.equal(outs[0].view(torch.int16), ref.view(torch.int16))
+            # the persistent GEMM (and its SiLU epilogue) alone, same tiles
+            takes = cfg is not None and (fq.w8a8_mm_silu_mul_supported(m, n, k, cfg) if silu
+                                         else kernel_supported(m, n, k, cfg))
+            if takes:
+                alone = [(fq.w8a8_mm_silu_mul(q, w.t(), s, sb, config=cfg) if silu
+                          else w8a8_mm(q, w.t(), s, sb, torch.bfloat16, config=cfg))
+                         for _ in range(40)]
+                torch.cuda.synchronize()
+                assert all(torch.equal(a.view(torch.int16), ref.view(torch.int16)) for a in alone)
