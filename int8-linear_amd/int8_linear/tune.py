@@ -185,21 +185,23 @@ def time_cold_us(call, copies: int, windows: int = 3) -> float:
     return statistics.median(res)
 
 
-def refine_candidates(m: int, k: int, n: int) -> list[Config]:
-    """The configuration tuned_config holds now (else the default) and the schedules that
-    changed after the table was made: every weights-through-LDS tile (stages 3: 64-column
-    tiles, 8 or more waves now that the reduction area shares the ring, activations copied
-    through LDS) and the split of K (stages 5).  Timing only these against the entry they
-    would replace updates a table without re-timing every candidate of every bucket."""
+def refine_candidates(m: int, k: int, n: int, stages=(3, 5)) -> list[Config]:
+    """The configuration tuned_config holds now (else the default) and the decode schedules of
+    the given stages that changed after the table was made: by default every
+    weights-through-LDS tile (stages 3: 64-column tiles, 8 or more waves now that the
+    reduction area shares the ring, activations copied through LDS) and the split of K
+    (stages 5); stages 4 is the persistent tile (its cross-wave exchanges no longer wait for
+    the next tile's weights).  Timing only these against the entry they would replace updates
+    a table without re-timing every candidate of every bucket."""
     from int8_linear.kernel import tuned_config
     cur = tuned_config(m, n, k) or default_config(m, n, k)
-    # stages 3 and 5 with bn <= 64; wider tiles at those stages are prefill rings (gemm_dma)
-    new = [c for c in candidate_configs(m, k, n) if c.stages in (3, 5) and c.bn <= 64]
+    # bn <= 64 at stages 3-5: wider tiles at those stages are prefill rings (gemm_dma)
+    new = [c for c in candidate_configs(m, k, n) if c.stages in stages and c.bn <= 64]
     return [cur] + [c for c in new if c != cur]
 
 
 def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = False,
-               min_gain: float = 0.0) -> dict:
+               min_gain: float = 0.0, refine_stages=(3, 5)) -> dict:
     """{str(M): {"config": {...}, "graph_us": t, "default_us": t0}} for one weight shape.
 
     The configuration the stored table gives now (tuned_config) is always among the
@@ -219,7 +221,8 @@ def tune_shape(k: int, n: int, ms: list[int], device, log=print, refine: bool = 
         ref = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=default_config(m, n, k))
         t0 = None
         timed = []
-        for cfg in (refine_candidates(m, k, n) if refine else candidate_configs(m, k, n)):
+        for cfg in (refine_candidates(m, k, n, refine_stages) if refine
+                    else candidate_configs(m, k, n)):
             got = w8a8_mm(a_q, ws[0].t(), one, one, raw=True, config=cfg)
             if not torch.equal(got, ref):
                 raise RuntimeError(f"config {cfg.name} gives a different product at M={m} K={k} N={n}")
@@ -364,6 +367,9 @@ def main() -> int:
     ap.add_argument("--refine", action="store_true",
                     help="time only the current table entry against the weights-through-LDS "
                          "tiles and the split of K (stages 3 and 5)")
+    ap.add_argument("--refine-stages", default="3,5",
+                    help="with --refine: the stages whose tiles are timed against the entry "
+                         "(comma-separated; 4 = the persistent decode tile)")
     ap.add_argument("--min-gain", type=float, default=0.0,
                     help="keep the stored entry unless a candidate is this fraction faster "
                          "(e.g. 0.02)")
@@ -384,7 +390,9 @@ def main() -> int:
         if only is not None and f"{k}x{n}" not in only:
             continue
         table[f"{k}x{n}"] = tune_shape(k, n, ms, dev, log=lambda *a: print(*a, file=sys.stderr, flush=True),
-                                       refine=args.refine, min_gain=args.min_gain)
+                                       refine=args.refine, min_gain=args.min_gain,
+                                       refine_stages=tuple(int(x) for x in
+                                                           args.refine_stages.split(",")))
     if args.out:
         with open(args.out, "w") as f:
             json.dump({arch: table}, f, indent=1)
