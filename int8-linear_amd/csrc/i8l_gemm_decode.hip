@@ -775,8 +775,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
   int8_t* wbuf = lds + (size_t)wave * SB;
   v4i* red = (v4i*)(lds + (size_t)W * SB);                          // [W][NF][64]
   float* rmax = (float*)(lds + (size_t)W * SB + (size_t)W * NF * 1024);  // [W][16]
-  float* scl = rmax + W * 16;               // [W][16]: each wave's copy of the row scales
-  int8_t* abuf = lds + (size_t)W * SB + (size_t)W * NF * 1024 + (size_t)W * 128 + wave * 16 * S;
+  int8_t* abuf = lds + (size_t)W * SB + (size_t)W * NF * 1024 + (size_t)W * 64 + wave * 16 * S;
 
   // The activations are requested first and waited for alone: the quantizer work below
   // then runs while the weights' DMA is still in flight.
@@ -862,24 +861,30 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
     if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
   }
   lds_sync();
-  auto row_scale = [&](int r, float& scale, float& inv) {
-    float absmax = rmax[r];
+  // each row's scale and inverse once, in lane r of every wave for row r (r = lane % 16,
+  // rows past the passes clamped to the last); a pass takes its row's from that lane
+  float sc_l, inv_l;
+  {
+    const int rl = min(r16, P * RPP - 1);
+    float absmax = rmax[rl];
 #pragma unroll
-    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + r]);
+    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + rl]);
     const float s_div = absmax / 127.0f;
     const float i_div = absmax == 0.0f ? 0.0f : 127.0f / absmax;
     const float s_rcp = absmax * (1.0f / 127.0f);
     const float i_rcp = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
-    scale = precise ? s_div : s_rcp;
-    inv = precise ? i_div : i_rcp;
-  };
+    sc_l = precise ? s_div : s_rcp;
+    inv_l = precise ? i_div : i_rcp;
+  }
+  if (sa_out != nullptr && blockIdx.x == 0 && wave == 0 && lane < mb) sa_out[m0 + lane] = sc_l;
   // codes of each valid chunk into the wave's LDS tile (row pitch S bytes)
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = p * RPP + crow;
+    float inv;
+    if constexpr (RPP == 1) inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l), p));
+    else inv = __shfl(inv_l, r);
     if (r < mb) {
-      float scale, inv;
-      row_scale(r, scale, inv);
       uint32_t word[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -893,10 +898,6 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
         word[q] = packed;
       }
       *(uint2*)(abuf + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
-      if (cchunk == 0) {
-        scl[wave * 16 + r] = scale;
-        if (sa_out != nullptr && blockIdx.x == 0 && wave == 0) sa_out[m0 + r] = scale;
-      }
     }
   }
   Cols4 cl;
@@ -934,8 +935,8 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
     v4i sum = red[wave * 64 + lane];
 #pragma unroll
     for (int w = 1; w < W; ++w) sum += red[(w * NF + wave) * 64 + lane];
-    // this wave's own scale of row r16 (written above by this wave: LDS is in order)
-    if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, scl[wave * 16 + r16]);
+    // row r16's scale: this lane computed it above (lane l holds row l % 16)
+    if (r16 < mb && 4 * grp < NCF) store4s<EK>(e, mrow, ncol, sum, cl, sc_l);
   }
 }
 
@@ -1423,8 +1424,8 @@ constexpr int kDqSiluMaxRows = 8;
 
 size_t dq_lds_bytes(int nc, int ks, int W) {
   const int nf = nc > 16 ? nc / 16 : 1;
-  // weights, the cross-wave sums, the row maxima and scales, the 16-row code tiles
-  return (size_t)W * nc * 64 * ks + (size_t)W * nf * 1024 + (size_t)W * 128 +
+  // weights, the cross-wave sums, the row maxima, the 16-row code tiles
+  return (size_t)W * nc * 64 * ks + (size_t)W * nf * 1024 + (size_t)W * 64 +
          (size_t)W * 16 * 64 * ks;
 }
 

@@ -24,7 +24,8 @@
 //     nodes pairwise through LDS (K = W*S is a power of two, the waves' slices are aligned
 //     nodes);
 //   * rsqrt, the two roundings of the norm, the row's absmax across lanes and waves, scale
-//     and codes exactly as add_rmsnorm_quant_kernel computes them;
+//     and codes exactly as add_rmsnorm_quant_kernel computes them (a row's rsqrt and scale
+//     once, in the lane of that row, not in every pass);
 //   * the codes go to an LDS tile of the wave's own, which aliases the wave's second weight
 //     buffer (not yet in use), and come back as the wave's MFMA activation fragments, held in
 //     registers for every column tile the workgroup takes.
@@ -89,7 +90,6 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   v4i* const red = (v4i*)(lds + (size_t)2 * W * SB);   // [W][NF][64]
   double* const dsum = (double*)(lds + (size_t)2 * W * SB + (size_t)W * NF * 1024);  // [W][16]
   float* const rmax = (float*)(dsum + W * 16);          // [W][16]
-  float* const scl = rmax + W * 16;                     // [W][16]: each wave's copy
   const int ldb32 = (int)ldb;
 
   auto dma = [&](int ct, int8_t* wb) {
@@ -161,22 +161,36 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   }
   lds_sync();
 
-  // the row's sum over the waves' nodes, rsqrt, y = cast(f32(cast(x * rs)) * gamma), and the
-  // row's absmax
-  float gv[8];
-  unpack8_act<DT>(gr, gv);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int r = p * RPP + crow;
+  // Each row's scalar work is done once, in lane r of every wave for row r (r = lane % 16,
+  // rows past the passes clamped to the last): the sum over the waves' nodes and the rsqrt
+  // here, the absmax over the waves and the scale below.  A pass takes its row's values from
+  // that lane, so the per-row division and square-root chains are not repeated P times.
+  const int rl = min(r16, P * RPP - 1);
+  float rs_l;
+  {
     double nd[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) nd[w] = dsum[w * 16 + r];
+    for (int w = 0; w < W; ++w) nd[w] = dsum[w * 16 + rl];
 #pragma unroll
     for (int st = 1; st < W; st <<= 1)
 #pragma unroll
       for (int w = 0; w < W; w += 2 * st) nd[w] = nd[w] + nd[w + st];
     const float var = (float)(nd[0] / (double)K);
-    const float rs = canon_rsqrtf(var + eps);
+    rs_l = canon_rsqrtf(var + eps);
+  }
+  // pass p's row value from lane r: a readlane when the pass is one row, else a permute
+  auto row_val = [&](float v, int p) {
+    if constexpr (RPP == 1) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), p));
+    else return __shfl(v, p * RPP + crow);
+  };
+
+  // y = cast(f32(cast(x * rs)) * gamma), and the row's absmax
+  float gv[8];
+  unpack8_act<DT>(gr, gv);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = p * RPP + crow;
+    const float rs = row_val(rs_l, p);
     float am = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
@@ -194,19 +208,26 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   }
   lds_sync();
 
-  // scale and codes (the quantizer of add_rmsnorm_quant_kernel), codes into the code tile
+  // scale and inverse of row rl (the quantizer of add_rmsnorm_quant_kernel)
+  float sc_l, inv_l;
+  {
+    float absmax = rmax[rl];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int r = p * RPP + crow;
-    float absmax = rmax[r];
-#pragma unroll
-    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + r]);
+    for (int w = 1; w < W; ++w) absmax = fmaxf(absmax, rmax[w * 16 + rl]);
     const float s_div = absmax / 127.0f;
     const float i_div = absmax == 0.0f ? 0.0f : 127.0f / absmax;
     const float s_rcp = absmax * (1.0f / 127.0f);
     const float i_rcp = absmax == 0.0f ? 0.0f : 127.0f * (1.0f / absmax);
-    const float scale = precise ? s_div : s_rcp;
-    const float inv = precise ? i_div : i_rcp;
+    sc_l = precise ? s_div : s_rcp;
+    inv_l = precise ? i_div : i_rcp;
+  }
+  if (sa_out != nullptr && blockIdx.x == 0 && wave == 0 && lane < mb) sa_out[lane] = sc_l;
+
+  // codes into the code tile
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int r = p * RPP + crow;
+    const float inv = row_val(inv_l, p);
     if (r < mb) {
       uint32_t word[2];
 #pragma unroll
@@ -221,10 +242,6 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
         word[h] = packed;
       }
       *(uint2*)(wb1 + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
-      if (cchunk == 0) {
-        scl[wave * 16 + r] = scale;
-        if (sa_out != nullptr && blockIdx.x == 0 && wave == 0) sa_out[r] = scale;
-      }
     }
   }
   // the wave's activation fragments from its own code tile (LDS is in order within a wave;
@@ -233,7 +250,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
 #pragma unroll
   for (int s = 0; s < KS; ++s)
     a[s] = r16 < mb ? *(const v4i*)(wb1 + r16 * S + 64 * s + 16 * grp) : v4i{0, 0, 0, 0};
-  const float sam = wave < NF && r16 < mb ? scl[wave * 16 + r16] : 0.0f;
+  const float sam = wave < NF && r16 < mb ? sc_l : 0.0f;   // lane l computed row l % 16
   wait_lgkmcnt0();                          // the code tile is read before wb1 is refilled
 
   int ct = blockIdx.x;
@@ -299,8 +316,8 @@ int nq_max_rows() { return kNqMaxRows; }
 
 static size_t nq_lds_bytes(int nc, int ks, int w) {
   const int nf = nc > 16 ? nc / 16 : 1;
-  // two weight buffers a wave, the cross-wave sums, the row nodes, maxima and scales
-  return (size_t)2 * w * nc * 64 * ks + (size_t)w * nf * 1024 + (size_t)w * 16 * (8 + 4 + 4);
+  // two weight buffers a wave, the cross-wave sums, the row nodes and maxima
+  return (size_t)2 * w * nc * 64 * ks + (size_t)w * nf * 1024 + (size_t)w * 16 * (8 + 4);
 }
 
 // stages 4 (persistent), bm 16; group_m workgroups a compute unit (1, 2 or 4).

@@ -269,11 +269,11 @@ def silu_mul_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 NORM_MM_MAX_M = 8
 # Largest M for which the decoder stand-in folds the norm into its projections.  Every
 # workgroup repeats the row work, so the fold pays only for few tokens: measured on MI355X
-# (HIP graph, cold weights, K = 2048), one launch against add_rmsnorm_quant + w8a8_mm at
-# N = 4096 is 3.79 / 4.31 / 5.90 / 6.13 / 8.32 us against 5.98 / 6.13 / 6.38 / 6.37 / 6.39 us
-# at 1 / 2 / 3 / 4 / 8 tokens, at N = 12288 6.03 / 6.48 / 8.15 / 8.28 / 12.10 against
-# 8.59 / 8.85 / 8.84 / 9.00 / 9.09 us; in the 28-layer stand-in the folds lose from 5 tokens
-# (29.68 us a layer unfolded at 5 against 33.29 folded).
+# (HIP graph, cold weights, K = 2048), the folded launch takes 3.68 / 3.94 / 5.12 / 5.71 /
+# 7.09 us at N = 4096 and 1 / 2 / 3 / 4 / 8 tokens, against 5.98 / 6.13 / 6.38 / 6.37 / 6.39
+# for add_rmsnorm_quant + w8a8_mm, and 6.01 / 6.50 / 7.65 / 7.80 / 10.32 at N = 12288 against
+# 8.59 / 8.85 / 8.84 / 9.00 / 9.09; in the 28-layer stand-in the folds lose from 5 tokens
+# (28.58 us a layer unfolded at 5 against 30.25 folded, 30.00 against 31.71 at 8).
 NORM_MM_FOLD_M = 4
 
 
@@ -345,10 +345,11 @@ def add_rmsnorm_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 # Token counts for which the decoder stand-in computes the SiLU-and-mul in gate_up_proj's
 # epilogue and folds the quantizer into down_proj (the kernel takes up to 16 tokens).
 # Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with the norm folded
-# in, with / without: 20.35 / 20.21 at 1 token (where silu_mul_quant_mm folds the whole SiLU
-# chain into down_proj instead), 22.06 / 23.46 at 2, 26.09 / 26.90 at 3, 26.92 / 27.44 at 4;
-# from 5 tokens no fold pays (29.68 us a layer at 5 unfolded against 33.29 with the norm
-# folded and 34.69 with both): every CU repeats the row work of each folded quantizer.
+# in, with / without: 19.62 / 19.82 at 1 token (where silu_mul_quant_mm folds the whole SiLU
+# chain into down_proj instead; the two are within the run-to-run spread, and an earlier run
+# had them the other way round), 21.06 / 22.01 at 2, 24.02 / 25.75 at 3, 24.89 / 26.11 at 4;
+# from 5 tokens no fold pays (28.58 us a layer at 5 unfolded against 30.25 with the norm
+# folded and 30.27 with both): every CU repeats the row work of each folded quantizer.
 SILU_EPI_MIN_M = 2
 SILU_EPI_MAX_M = 4
 
