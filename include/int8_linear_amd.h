@@ -164,6 +164,17 @@ int i8l_w8a8_mm_noalloc(const int8_t* a, int64_t stride_am, int64_t stride_ak,
                         const i8l_config* cfg, void* stream);
 
 /*
+ * Library set-up on one GPU (device -1: the calling thread's current device): looks up the
+ * device address of i8l_w8a8_mm_noalloc's scratch array there, with that device made
+ * current and the thread's previous current device restored before returning.  Optional:
+ * i8l_w8a8_mm_noalloc does the same on its first call on a device otherwise.  Call it once
+ * per GPU at set-up, before any HIP graph capture, so that no later call switches devices
+ * or looks up a symbol.  Allocates nothing beyond the array the library holds on every GPU
+ * it runs on.  No counterpart in the reference; host-only, safe to call more than once.
+ */
+int i8l_init(int32_t device);
+
+/*
  * Whether i8l_w8a8_mm takes this (M,N,K,cfg) on a fast schedule: returns I8L_OK or
  * I8L_UNSUPPORTED without launching anything (host-only; no GPU needed).  The decline
  * rule is the reference's: N % bn or K % bk non-zero (int8_linear/kernel.py:228-229),

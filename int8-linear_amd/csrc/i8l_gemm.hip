@@ -794,31 +794,28 @@ static __device__ __align__(256) int32_t scratch[kScratchBytes / 4];
 constexpr int kScratchDevices = 64;
 static std::atomic<void*> g_scratch[kScratchDevices];
 
-// The device address of `scratch` on the GPU that runs `stream`, looked up once per device
-// with that device current (in host code the array's name stands for the symbol, not for
-// device memory).
-static int scratch_address(hipStream_t stream, void** out) {
-  int dev = 0;
-  hipError_t e = hipStreamGetDevice(stream, &dev);
-  if (e != hipSuccess) return hip_status(e, "i8l_w8a8_mm_noalloc: hipStreamGetDevice");
+// The device address of `scratch` on device `dev`, looked up once per device with that device
+// current (in host code the array's name stands for the symbol, not for device memory); the
+// calling thread's current device is restored.
+static int scratch_setup(int dev, void** out, const char* where) {
   if (dev < 0 || dev >= kScratchDevices) {
-    set_error("i8l_w8a8_mm_noalloc: device %d is beyond the %d this library serves", dev,
+    set_error("%s: device %d is beyond the %d this library serves", where, dev,
               kScratchDevices);
     return I8L_UNSUPPORTED;
   }
   void* p = g_scratch[dev].load(std::memory_order_acquire);
   if (!p) {
     int cur = 0;
-    e = hipGetDevice(&cur);
+    hipError_t e = hipGetDevice(&cur);
     if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
     if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (cur != dev) {
       const hipError_t r = hipSetDevice(cur);
       if (e == hipSuccess) e = r;
     }
-    if (e != hipSuccess) return hip_status(e, "i8l_w8a8_mm_noalloc: hipGetSymbolAddress");
+    if (e != hipSuccess) return hip_status(e, where);
     if (!p) {
-      set_error("i8l_w8a8_mm_noalloc: no device address for the scratch array");
+      set_error("%s: no device address for the scratch array", where);
       return I8L_HIP_ERROR;
     }
     g_scratch[dev].store(p, std::memory_order_release);
@@ -827,7 +824,33 @@ static int scratch_address(hipStream_t stream, void** out) {
   return I8L_OK;
 }
 
+// The scratch address on the GPU that runs `stream` (set up by i8l_init, else here).
+static int scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  const hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_status(e, "i8l_w8a8_mm_noalloc: hipStreamGetDevice");
+  return scratch_setup(dev, out, "i8l_w8a8_mm_noalloc");
+}
+
 }  // namespace i8l
+
+extern "C" int i8l_init(int32_t device) {
+  int dev = device;
+  if (dev < 0) {
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "i8l_init: hipGetDevice");
+  } else {
+    int count = 0;
+    const hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_status(e, "i8l_init: hipGetDeviceCount");
+    if (dev >= count) {
+      set_error("i8l_init: device %d of %d", dev, count);
+      return I8L_INVALID_ARG;
+    }
+  }
+  void* p = nullptr;
+  return scratch_setup(dev, &p, "i8l_init");
+}
 
 extern "C" int i8l_w8a8_mm_noalloc(const int8_t* a, int64_t stride_am, int64_t stride_ak,
                                    const int8_t* b, int64_t stride_bk, int64_t stride_bn,

@@ -34,7 +34,7 @@ EXPORTS = ("i8l_w8a8_mm", "i8l_w8a8_mm_supported", "i8l_default_config",
            "i8l_add_rmsnorm_quant", "i8l_silu_mul_quant", "i8l_quant_per_token",
            "i8l_w8a8_mm_dynq", "i8l_w8a8_mm_dynq_supported",
            "i8l_silu_mul_quant_mm", "i8l_silu_mul_quant_mm_supported", "i8l_w8a8_mm_ws",
-           "i8l_w8a8_mm_workspace_bytes", "i8l_w8a8_mm_noalloc",
+           "i8l_w8a8_mm_workspace_bytes", "i8l_w8a8_mm_noalloc", "i8l_init",
            "i8l_add_rmsnorm_quant_mm", "i8l_add_rmsnorm_quant_mm_supported",
            "i8l_w8a8_mm_silu_mul", "i8l_w8a8_mm_silu_mul_supported", "i8l_last_error",
            "i8l_version")
@@ -72,6 +72,7 @@ def lib() -> ctypes.CDLL:
         L.i8l_w8a8_mm.argtypes[-2:]
     L.i8l_w8a8_mm_workspace_bytes.argtypes = [_I64, _I64, _I64, ctypes.POINTER(CConfig)]
     L.i8l_w8a8_mm_noalloc.argtypes = L.i8l_w8a8_mm.argtypes
+    L.i8l_init.argtypes = [_I32]
     L.i8l_add_rmsnorm_quant_mm.argtypes = [_P, _P, _P, ctypes.c_float, _I32, _I32, _I32, _P, _P,
                                            _I64, _I64, _P, _I64, _P, _I32, _P, _I64, _I32, _P,
                                            _I64, _I64, _I64, ctypes.POINTER(CConfig), _P]

@@ -249,6 +249,18 @@ def w8a8_mm(
     return out
 
 
+def init(device: torch.device | int | None = None) -> None:
+    """Set up the library on one GPU (default: the current one): the C entry i8l_init, which
+    looks up the device address of the array w8a8_mm_noalloc keeps its split-of-K partials
+    in.  Optional (the first w8a8_mm_noalloc call on a GPU does it otherwise); call it before
+    capturing that first call into a HIP graph.  No counterpart in the reference."""
+    idx = -1
+    if device is not None:
+        d = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        idx = -1 if d.index is None else d.index
+    _lib.check(_lib.lib().i8l_init(idx), NotSupported)
+
+
 def w8a8_mm_noalloc(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
                     scale_b: torch.Tensor, out: torch.Tensor, bias: torch.Tensor | None = None,
                     *, config: Config | None = None) -> torch.Tensor:
@@ -263,6 +275,7 @@ def w8a8_mm_noalloc(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,
     on it and give wrong results: order them (one stream, or events).  Configurations whose
     planes exceed 16 MiB raise NotSupported (use w8a8_mm).  Scales and bias are taken as they
     are: contiguous float32 scales and a contiguous bias, or ValueError (no copies are made).
+    The first call on a GPU looks up that array's device address unless init() did.
     """
     if a_q.dtype != torch.int8 or b_q.dtype != torch.int8:
         raise NotSupported(f"int8 operands only, got {a_q.dtype} and {b_q.dtype}")

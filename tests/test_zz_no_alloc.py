@@ -87,6 +87,8 @@ def test_noalloc_declines_beyond_its_scratch_and_runs_unsplit_configs():
 def test_python_wrapper_matches_w8a8_mm():
     """int8_linear.kernel.w8a8_mm_noalloc (into the caller's out) gives w8a8_mm's bits, with
     a split of K and without, and refuses operands it would have to copy."""
+    kernel.init()                             # the set-up entry, current GPU and by index
+    kernel.init(torch.cuda.current_device())
     k, n = 6144, 2048
     w = ints((n, k), 71)
     g = torch.Generator().manual_seed(72)
@@ -105,8 +107,9 @@ def test_python_wrapper_matches_w8a8_mm():
 
 
 # A fresh process whose first use of the library is an allocation-free split-of-K call under
-# HIP graph capture (so the device's scratch address is looked up inside the capture), then
-# replays with new activations checked against the workspace entry.
+# HIP graph capture (so the device's scratch address is looked up inside the capture, unless
+# argv[2] is "init": then i8l_init sets the device up before the capture), then replays with
+# new activations checked against the workspace entry.
 _CAPTURE = r"""
 import ctypes, sys
 sys.path[:0] = [sys.argv[1], sys.argv[1] + "/int8-linear_amd"]
@@ -127,6 +130,11 @@ def call(entry, o, *ws):
     return entry(a.data_ptr(), k, 1, w.data_ptr(), 1, k, sa.data_ptr(), m, sb.data_ptr(), n,
                  None, _lib.DTYPE_NONE, o.data_ptr(), n, _lib.BF16, m, n, k, *ws,
                  ctypes.byref(c), torch.cuda.current_stream().cuda_stream)
+if sys.argv[2] == "init":
+    assert L.i8l_init(-1) == _lib.OK, _lib.last_error()
+    assert L.i8l_init(0) == _lib.OK, _lib.last_error()       # again, by index: no-op
+    assert L.i8l_init(torch.cuda.device_count()) == _lib.INVALID_ARG
+    print("init", flush=True)
 graph = torch.cuda.CUDAGraph()
 with torch.cuda.graph(graph):
     st = call(L.i8l_w8a8_mm_noalloc, out)
@@ -148,13 +156,14 @@ print("ok", flush=True)
 """
 
 
-def test_first_call_inside_a_graph_capture():
+@pytest.mark.parametrize("setup", ["lazy", "init"])
+def test_first_call_inside_a_graph_capture(setup):
     import subprocess
     import sys
     from pathlib import Path
     root = str(Path(__file__).resolve().parents[1])
-    say("noalloc: first call of a fresh process under graph capture, 4 replays")
-    r = subprocess.run([sys.executable, "-c", _CAPTURE, root], capture_output=True, text=True,
-                       timeout=150)
+    say(f"noalloc: first call of a fresh process under graph capture ({setup}), 4 replays")
+    r = subprocess.run([sys.executable, "-c", _CAPTURE, root, setup], capture_output=True,
+                       text=True, timeout=150)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), (r.stdout[-2000:],
                                                                   r.stderr[-2000:])
