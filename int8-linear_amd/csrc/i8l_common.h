@@ -181,6 +181,53 @@ __device__ __forceinline__ double group_tree_sum(double v) {
   return v;
 }
 
+// group_tree_sum of N independent values, level by level across the values, so that the
+// cross-lane moves of one value overlap the additions of the others (each value's sum is
+// the same tree, bit for bit).
+template <int G, int N>
+__device__ __forceinline__ void group_tree_sum_n(double (&v)[N]) {
+  static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_d<kQuadSwap1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_d<kQuadSwap2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_d<kHalfMirror>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_d<kRowMirror>(v[i]);
+  if constexpr (G >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + swz16_d(v[i]);
+  }
+  if constexpr (G == 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = readlane_d(v[i], 0) + readlane_d(v[i], 32);
+  }
+}
+
+// group_max of N independent values, level by level across the values.
+template <int G, int N>
+__device__ __forceinline__ void group_max_n(float (&v)[N]) {
+  static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<kQuadSwap1>(__float_as_int(v[i]))));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<kQuadSwap2>(__float_as_int(v[i]))));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<kHalfMirror>(__float_as_int(v[i]))));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<kRowMirror>(__float_as_int(v[i]))));
+  if constexpr (G >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      v[i] = fmaxf(v[i], __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), kSwizzleXor16)));
+  }
+  if constexpr (G == 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __shfl_xor(v[i], 32));
+  }
+}
+
 // ---------------------------------------------------------------- errors
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* where);

@@ -807,6 +807,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
   }
   __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt_wlds<NI>();  // vector loads complete in issue order: the activations are in
+  __builtin_amdgcn_sched_barrier(0);        // no use of the rows above the wait
 
   auto elem = [&](const uint4& v, int k) -> float {
     const uint32_t w32 = k < 4 ? (k < 2 ? v.x : v.y) : (k < 6 ? v.z : v.w);
@@ -851,14 +852,19 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
   } else {
     fill(false);
   }
-  // absmax of each valid row's slice: a lane's chunk, then the CH lanes of the row
+  // absmax of each valid row's slice: a lane's chunk, then the CH lanes of the row (the
+  // passes' cross-lane maxima side by side)
+  float am[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    float am = 0.0f;
+    am[p] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(y[p][k]));
-    am = group_max<CH>(am);
-    if (cchunk == 0) rmax[wave * 16 + p * RPP + crow] = am;
+    for (int k = 0; k < 8; ++k) am[p] = fmaxf(am[p], fabsf(y[p][k]));
+  }
+  group_max_n<CH, P>(am);
+  if (cchunk == 0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) rmax[wave * 16 + p * RPP + crow] = am[p];
   }
   lds_sync();
   // each row's scale and inverse once, in lane r of every wave for row r (r = lane % 16,
@@ -877,13 +883,18 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
     inv_l = precise ? i_div : i_rcp;
   }
   if (sa_out != nullptr && blockIdx.x == 0 && wave == 0 && lane < mb) sa_out[m0 + lane] = sc_l;
-  // codes of each valid chunk into the wave's LDS tile (row pitch S bytes)
+  // codes of each valid chunk into the wave's LDS tile (row pitch S bytes); the passes'
+  // inverses fetched first, together
+  float invp[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    if constexpr (RPP == 1) invp[p] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l), p));
+    else invp[p] = __shfl(inv_l, p * RPP + crow);
+  }
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = p * RPP + crow;
-    float inv;
-    if constexpr (RPP == 1) inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l), p));
-    else inv = __shfl(inv_l, r);
+    const float inv = invp[p];
     if (r < mb) {
       uint32_t word[2];
 #pragma unroll

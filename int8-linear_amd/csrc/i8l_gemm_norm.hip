@@ -126,24 +126,20 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   dma(blockIdx.x, wb0);                     // the first tile's weights, while the rows work
   __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt_wlds<NI>();                    // loads land in issue order: the rows are in
+  __builtin_amdgcn_sched_barrier(0);        // no use of the rows above the wait
 
-  // x (+ residual), residual_out, and each row's node of the sum of squares
+  // x (+ residual) and each row's node of the sum of squares, the passes' cross-lane trees
+  // side by side; then residual_out (first workgroup only)
   float xv[P][8];
+  double node[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int r = p * RPP + crow;
     unpack8_act<DT>(xr[p], xv[p]);
     if constexpr (RES) {
       float rv[8];
       unpack8_act<DT>(rr[p], rv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[p][i] = xv[p][i] + rv[i];
-      if (blockIdx.x == 0 && r < mb) {
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = f32x2_to_act2<DT>(xv[p][2 * i], xv[p][2 * i + 1]);
-        *(uint4*)(rout + (int64_t)r * K + c0) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
     }
     // leaves x_i^2 are exact in double, so x_i^2 + x_{i+1}^2 is one fma
     double s[8];
@@ -156,8 +152,26 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
     for (int st = 2; st < 8; st <<= 1)
 #pragma unroll
       for (int i = 0; i < 8; i += 2 * st) s[i] = s[i] + s[i + st];
-    const double node = group_tree_sum<CH>(s[0]);
-    if (cchunk == 0) dsum[wave * 16 + r] = node;
+    node[p] = s[0];
+  }
+  group_tree_sum_n<CH, P>(node);
+  if (cchunk == 0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) dsum[wave * 16 + p * RPP + crow] = node[p];
+  }
+  if constexpr (RES) {
+    if (blockIdx.x == 0) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int r = p * RPP + crow;
+        if (r < mb) {
+          uint32_t w[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = f32x2_to_act2<DT>(xv[p][2 * i], xv[p][2 * i + 1]);
+          *(uint4*)(rout + (int64_t)r * K + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    }
   }
   lds_sync();
 
@@ -184,14 +198,17 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
     else return __shfl(v, p * RPP + crow);
   };
 
-  // y = cast(f32(cast(x * rs)) * gamma), and the row's absmax
+  // y = cast(f32(cast(x * rs)) * gamma), and the row's absmax (the passes' cross-lane
+  // maxima side by side)
   float gv[8];
   unpack8_act<DT>(gr, gv);
+  float am[P], rsp[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) rsp[p] = row_val(rs_l, p);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int r = p * RPP + crow;
-    const float rs = row_val(rs_l, p);
-    float am = 0.0f;
+    const float rs = rsp[p];
+    am[p] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
       float a = xv[p][i] * rs, b = xv[p][i + 1] * rs;
@@ -201,10 +218,13 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       round_through2<DT>(a, b);
       xv[p][i] = a;
       xv[p][i + 1] = b;
-      am = fmaxf(am, fmaxf(fabsf(a), fabsf(b)));
+      am[p] = fmaxf(am[p], fmaxf(fabsf(a), fabsf(b)));
     }
-    am = group_max<CH>(am);
-    if (cchunk == 0) rmax[wave * 16 + r] = am;
+  }
+  group_max_n<CH, P>(am);
+  if (cchunk == 0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) rmax[wave * 16 + p * RPP + crow] = am[p];
   }
   lds_sync();
 
@@ -223,11 +243,14 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   }
   if (sa_out != nullptr && blockIdx.x == 0 && wave == 0 && lane < mb) sa_out[lane] = sc_l;
 
-  // codes into the code tile
+  // codes into the code tile (the passes' inverses fetched first, together)
+  float invp[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) invp[p] = row_val(inv_l, p);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int r = p * RPP + crow;
-    const float inv = row_val(inv_l, p);
+    const float inv = invp[p];
     if (r < mb) {
       uint32_t word[2];
 #pragma unroll
@@ -333,21 +356,27 @@ bool nq_ok(const i8l_config& c, int64_t K) {
 }
 
 // The untuned choice, from a sweep of the built tiles on MI355X (K = 2048, N = 4096 and
-// 12288, 1-4 tokens, HIP graph, cold weights): 4 waves of 512-byte slices (the fewest passes
-// of the shortest prologue) for one token, and up to 3 tokens where every workgroup has one
-// tile (N = 4096 at 2 / 3 tokens: 4.25 / 5.85 us against 4.80 / 6.15 with 8 waves); otherwise
-// 8 waves of 256-byte slices (the row work spread over twice the lanes, N = 12288 at 2 / 3
-// tokens: 6.48 / 8.29 us against 6.61 / 8.80); 16 columns a tile (8 when N does not give 256
-// tiles of 16); two workgroups a compute unit where a workgroup would otherwise walk more
-// than one tile and the LDS holds two.  K = 4096 takes 8 waves of 512 bytes.
+// 12288, 1-8 tokens, HIP graph, cold weights): 4 waves of 512-byte slices wherever every
+// workgroup has one tile (N = 4096: 3.63 / 4.72 / 4.90 / 6.57 us at 1 / 3 / 4 / 8 tokens
+// against 4.81 / 5.03 / 5.15 / 6.71 with 8 waves) and up to 4 tokens otherwise, two
+// workgroups a compute unit (N = 12288 at 4 tokens: 7.51 us against 7.59 with 8 waves); from
+// 5 tokens with several tiles a workgroup, 8 waves of 256-byte slices, the row work spread
+// over twice the lanes, one workgroup a compute unit (N = 12288 at 5 / 8 tokens: 8.92 / 9.18
+// us against 9.52 / 10.24 with 4 waves, 9.20 / 9.93 with two workgroups); 16 columns a tile
+// (8 when N does not give 256 tiles of 16).  Two workgroups a compute unit only where a
+// workgroup would otherwise walk more than one tile and the LDS holds two.  K = 4096 takes
+// 8 waves of 512 bytes.
 bool default_nq_config(int64_t M, int64_t N, int64_t K, i8l_config* c) {
   const int nc = N % 16 == 0 && N / 16 >= 256 ? 16 : 8;
   static const int one[3][2] = {{512, 4}, {256, 8}, {512, 8}};    // (bk, waves) by preference
   static const int more[3][2] = {{256, 8}, {512, 4}, {512, 8}};
-  const bool one_tile = N / nc <= cu_count();
-  const int (&pref)[3][2] = M <= 1 || (M <= 3 && one_tile) ? one : more;
+  const bool few = N / nc <= cu_count() || M <= 4;
+  const int (&pref)[3][2] = few ? one : more;
+  static const int g_few[2] = {2, 1}, g_more[2] = {1, 2};
+  const int* gs = few ? g_few : g_more;
   for (const auto& bw : pref)
-    for (int g : {2, 1}) {
+    for (int gi = 0; gi < 2; ++gi) {
+      const int g = gs[gi];
       if (g == 2 && N / nc <= 256) continue;
       const i8l_config t{16, nc, bw[0], bw[1], 4, g};
       if (N % nc == 0 && nq_ok(t, K)) {

@@ -211,9 +211,11 @@ def quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 
 # Largest M that silu_mul_quant_mm takes.  Every column tile reads and computes the
 # SiLU-and-mul of its token rows (2K values a row), so the folded launch pays off only for
-# very few tokens: measured in the 28-layer Qwen3-1.7B stand-in on MI355X (graph replay),
-# 26.45 against 28.57 us a layer at M = 1, 28.22 against 28.80 at M = 2, but 32.15 against
-# 29.36 at M = 4 and 40.02 against 31.08 at M = 8 (the kernel itself takes up to 8 rows).
+# very few tokens: measured in the 28-layer Qwen3-1.7B stand-in on MI355X (graph replay, the
+# norm folded too), 19.28 against 21.56 us a layer at M = 1 and 20.95 against 23.06 at M = 2,
+# where the SiLU epilogue of gate_up does better still (20.34); earlier builds of the fold
+# lost at 4 and 8 tokens (32.15 against 29.36, 40.02 against 31.08; the kernel itself takes
+# up to 8 rows).
 SILU_MM_MAX_M = 2
 
 
@@ -269,11 +271,11 @@ def silu_mul_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 NORM_MM_MAX_M = 8
 # Largest M for which the decoder stand-in folds the norm into its projections.  Every
 # workgroup repeats the row work, so the fold pays only for few tokens: measured on MI355X
-# (HIP graph, cold weights, K = 2048), the folded launch takes 3.68 / 3.94 / 5.12 / 5.71 /
-# 7.09 us at N = 4096 and 1 / 2 / 3 / 4 / 8 tokens, against 5.98 / 6.13 / 6.38 / 6.37 / 6.39
-# for add_rmsnorm_quant + w8a8_mm, and 6.01 / 6.50 / 7.65 / 7.80 / 10.32 at N = 12288 against
+# (HIP graph, cold weights, K = 2048), the folded launch takes 3.64 / 4.17 / 4.83 / 4.89 /
+# 6.55 us at N = 4096 and 1 / 2 / 3 / 4 / 8 tokens, against 5.98 / 6.13 / 6.38 / 6.37 / 6.39
+# for add_rmsnorm_quant + w8a8_mm, and 5.96 / 6.16 / 7.19 / 7.51 / 9.21 at N = 12288 against
 # 8.59 / 8.85 / 8.84 / 9.00 / 9.09; in the 28-layer stand-in the folds lose from 5 tokens
-# (28.58 us a layer unfolded at 5 against 30.25 folded, 30.00 against 31.71 at 8).
+# (27.93 us a layer unfolded at 5 against 28.73 folded, 29.12 against 30.32 at 8).
 NORM_MM_FOLD_M = 4
 
 
@@ -344,14 +346,13 @@ def add_rmsnorm_quant_mm_supported(m: int, n: int, k: int, config=None) -> bool:
 
 # Token counts for which the decoder stand-in computes the SiLU-and-mul in gate_up_proj's
 # epilogue and folds the quantizer into down_proj (the kernel takes up to 16 tokens).
-# Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with the norm folded
-# in, with / without: 19.62 / 19.82 at 1 token (where silu_mul_quant_mm folds the whole SiLU
-# chain into down_proj instead; the two are within the run-to-run spread, and an earlier run
-# had them the other way round), 21.06 / 22.01 at 2, 24.02 / 25.75 at 3, 24.89 / 26.11 at 4;
-# from 5 tokens no fold pays (28.58 us a layer at 5 unfolded against 30.25 with the norm
-# folded and 30.27 with both): every CU repeats the row work of each folded quantizer.
+# Measured in the 28-layer stand-in on MI355X (graph replay), us a layer with / without:
+# with the norm folded too, 19.57 / 19.28 at 1 token (where silu_mul_quant_mm folds the whole
+# SiLU chain into down_proj instead), 20.34 / 20.95 at 2, 23.03 / 25.06 at 3, 23.88 / 25.58 at
+# 4; with the norm unfolded, 27.55 / 27.93 at 5, 28.19 / 28.04 at 6, 28.51 / 28.49 at 7 and
+# 28.94 / 29.12 at 8 (at 6-7 within the run-to-run spread).
 SILU_EPI_MIN_M = 2
-SILU_EPI_MAX_M = 4
+SILU_EPI_MAX_M = 8
 
 
 def w8a8_mm_silu_mul(a_q: torch.Tensor, b_q: torch.Tensor, scale_a: torch.Tensor,

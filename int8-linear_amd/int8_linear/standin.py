@@ -19,9 +19,10 @@ fused_quant.QUANT_MM_MAX_M tokens, the quantizer and o_proj are one kernel
 (fused_quant.quant_mm), and for the few tokens fused_quant.silu_mul_quant_mm takes,
 SiLU-and-mul+quant and down_proj are one kernel too, and up to
 fused_quant.NORM_MM_FOLD_M tokens each add+RMSNorm+quant is folded into the projection
-after it (fused_quant.add_rmsnorm_quant_mm), and at 2-4 tokens gate_up_proj writes
-silu(gate) * up itself (fused_quant.w8a8_mm_silu_mul) for down_proj to quantize; each gives
-the same bits as the kernels it replaces: 4 kernels a layer at 1-4 tokens.
+after it (fused_quant.add_rmsnorm_quant_mm), and from fused_quant.SILU_EPI_MIN_M to
+SILU_EPI_MAX_M tokens gate_up_proj writes silu(gate) * up itself
+(fused_quant.w8a8_mm_silu_mul) for down_proj to quantize; each gives the same bits as the
+kernels it replaces: 4 kernels a layer at 1-4 tokens, 6 at 5-8.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
