@@ -316,6 +316,23 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 
 typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 
+// A 16-byte LDS store written as inline assembly, so that the compiler does not see an LDS
+// store: with a direct-to-LDS copy in flight it would first wait for every vector-memory
+// request (it cannot tell that the copy writes elsewhere).  The caller must not store where
+// a copy in flight writes, and waits for the store itself (lgkmcnt, as lds_sync does) before
+// other waves read it.  The s_nops give the 19 wait states an MFMA result needs before a DS
+// instruction may read it (16-pass XDL operations need 18).
+__device__ __forceinline__ void lds_store_b128(void* p, v4i v) {
+  const uint32_t a = (uint32_t)(uintptr_t)(lds_i8_t*)p;
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4\n\tds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+// The same for 8 bytes written by ordinary VALU code (no MFMA wait states needed).
+__device__ __forceinline__ void lds_store_b64(void* p, uint32_t lo, uint32_t hi) {
+  const uint32_t a = (uint32_t)(uintptr_t)(lds_i8_t*)p;
+  const uint64_t v = (uint64_t)lo | ((uint64_t)hi << 32);
+  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+
 // Workgroup barrier for data the waves exchange through LDS stores (ds_write): each wave's
 // LDS operations have completed (lgkmcnt 0), then s_barrier.  Unlike __syncthreads() it does
 // not wait for the wave's outstanding global loads and direct-to-LDS copies (vmcnt), so a

@@ -585,7 +585,7 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
 // [t*H, (t+1)*H) and the same up rows (H = NC/2) into the fragment's first and last H rows,
 // and the epilogue writes y = silu(gate) * up, [M, N/2] bf16 (silu_mul_pairs), instead of the
 // [M, N] product.
-template <int MT, int NC, int KS, int W, int EK, int ACT = kActPlain>
+template <int MT, int NC, int KS, int W, int EK, int ACT = kActPlain, bool LOOP = true>
 __global__ void __launch_bounds__(64 * W)
 gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
             int64_t ldb, Epi e) {
@@ -658,24 +658,20 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   float sam = 0.0f;
   if (wave < FR) sam = load_sa<EK>(e, mrow < e.M ? mrow : m0);
 
-  int ct = blockIdx.x;
-  dma(ct, wb0);
-  for (int it = 0; ct < tiles; ++it, ct += gridDim.x) {
-    int8_t* const cur = (it & 1) ? wb1 : wb0;
-    const int64_t n0 = (int64_t)ct * NC;
-    const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
-    // SiLU: gate lanes (cq < H) read gate columns ct*H + cq, up lanes up columns N/2 + ...
-    const int64_t ncol = SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
-                              : n0 + NCF * (wave % NF) + cq;
-    Cols4 cl;
-    if (wave < FR) cl = load_cols4<EK>(e, ncol);
-    const bool more = ct + (int)gridDim.x < tiles;  // uniform over the workgroup
-    if (more) {
-      dma(ct + gridDim.x, (it & 1) ? wb0 : wb1);
-      wait_vmcnt_wlds<NI>();   // everything but the next tile's weights has landed
-    } else {
-      wait_vmcnt_wlds<0>();
-    }
+  const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
+  // SiLU: gate lanes (cq < H) read gate columns ct*H + cq, up lanes up columns N/2 + ...
+  auto ncol_of = [&](int ct) -> int64_t {
+    return SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
+                : (int64_t)ct * NC + NCF * (wave % NF) + cq;
+  };
+
+  // A tile's MFMAs, cross-wave sum and epilogue, from its weights in `cur` and its epilogue
+  // operands `cl` (both landed).  ASM: the reduction's LDS stores as inline assembly, for
+  // when the next tile's copy is in flight (an LDS store the compiler can see would make it
+  // wait for every vector-memory request first: it cannot tell where the copy writes).
+  auto body = [&](int ct, const int8_t* cur, const Cols4& cl, auto asm_tag) {
+    constexpr bool ASM = decltype(asm_tag)::value;
+    const int64_t ncol = ncol_of(ct);
     v4i b[KS][NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -699,7 +695,11 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) red[(wave * FR + i * NF + f) * 64 + lane] = acc[i][f];
+      for (int f = 0; f < NF; ++f) {
+        v4i* const slot = &red[(wave * FR + i * NF + f) * 64 + lane];
+        if constexpr (ASM) lds_store_b128(slot, acc[i][f]);
+        else *slot = acc[i][f];
+      }
     lds_sync();
     if (wave < FR) {
       v4i sum = red[wave * 64 + lane];
@@ -715,6 +715,47 @@ gemm_wlds1p(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
       }
     }
     lds_sync();  // the partials of the next tile overwrite the reduction area
+  };
+
+  int ct = blockIdx.x;
+  if (ct >= tiles) return;
+  if constexpr (!LOOP) {
+    // one tile a workgroup (the launcher's choice when the grid covers the tiles): nothing
+    // else is requested while it runs
+    dma(ct, wb0);
+    Cols4 cl;
+    if (wave < FR) cl = load_cols4<EK>(e, ncol_of(ct));
+    wait_vmcnt_wlds<0>();
+    body(ct, wb0, cl, std::false_type{});
+    return;
+  }
+  // Several tiles a workgroup.  A tile's weights and epilogue operands are requested a tile
+  // earlier; the explicit vmcnt(0) at the top of each tile is the loop's only wait on vector
+  // memory, after which the next tile's are requested, so they are in flight during this
+  // tile's MFMAs, reduction and epilogue.  (A use of a loaded register while a direct-to-LDS
+  // copy is in flight makes the compiler wait for every request, so the operands live in two
+  // register sets that alternate between tiles.)
+  auto tile = [&](int ct, const int8_t* cur, int8_t* nxt, const Cols4& cl, Cols4& cln) {
+    wait_vmcnt_wlds<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int ctn = ct + (int)gridDim.x;
+    if (ctn < tiles) {               // uniform over the workgroup
+      dma(ctn, nxt);
+      if (wave < FR) cln = load_cols4<EK>(e, ncol_of(ctn));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    body(ct, cur, cl, std::true_type{});
+  };
+  Cols4 c0, c1;
+  dma(ct, wb0);
+  if (wave < FR) c0 = load_cols4<EK>(e, ncol_of(ct));
+  for (;;) {
+    tile(ct, wb0, wb1, c0, c1);
+    ct += gridDim.x;
+    if (ct >= tiles) break;
+    tile(ct, wb1, wb0, c1, c0);
+    ct += gridDim.x;
+    if (ct >= tiles) break;
   }
 }
 
@@ -908,7 +949,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
         }
         word[q] = packed;
       }
-      *(uint2*)(abuf + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
+      lds_store_b64(abuf + r * S + 8 * cchunk, word[0], word[1]);  // the weight copy is in flight
     }
   }
   Cols4 cl;
@@ -1332,14 +1373,16 @@ int cu_count() {
 template <int MT, int NC, int KS, int W, int EK, int ACT = kActPlain>
 hipError_t launch_wldsp_k(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                           const Epi& e, int per_cu, hipStream_t st) {
-  auto kern = gemm_wlds1p<MT, NC, KS, W, EK, ACT>;
   const size_t shm = wldsp_lds_bytes(MT, NC, KS, W);
-  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
-  lds_opt_in((const void*)kern, shm, lds_done);
   const int rows = (e.M + 16 * MT - 1) / (16 * MT);
   const int tiles = e.N / NC;
   const int per_row = std::max(1, per_cu * cu_count() / rows);  // per_cu workgroups a CU
   const dim3 grid((unsigned)std::min(tiles, per_row), (unsigned)rows);
+  // the straight single-tile form where every workgroup has one tile, else the tile loop
+  const bool loop = tiles > (int)grid.x;
+  auto kern = loop ? gemm_wlds1p<MT, NC, KS, W, EK, ACT, true> : gemm_wlds1p<MT, NC, KS, W, EK, ACT, false>;
+  static std::atomic<uint64_t> lds_done_loop{0}, lds_done_one{0};  // devices opted in on
+  lds_opt_in((const void*)kern, shm, loop ? lds_done_loop : lds_done_one);
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), shm, st, a, lda, b, ldb, e);
   return hipGetLastError();
 }

@@ -264,7 +264,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
         }
         word[h] = packed;
       }
-      *(uint2*)(wb1 + r * S + 8 * cchunk) = make_uint2(word[0], word[1]);
+      lds_store_b64(wb1 + r * S + 8 * cchunk, word[0], word[1]);   // the first tile's copy is in flight
     }
   }
   // the wave's activation fragments from its own code tile (LDS is in order within a wave;
@@ -276,21 +276,26 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
   const float sam = wave < NF && r16 < mb ? sc_l : 0.0f;   // lane l computed row l % 16
   wait_lgkmcnt0();                          // the code tile is read before wb1 is refilled
 
-  int ct = blockIdx.x;
-  for (int it = 0; ct < tiles; ++it, ct += gridDim.x) {
-    int8_t* const cur = (it & 1) ? wb1 : wb0;
-    const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
-    const int64_t ncol = SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
-                              : (int64_t)ct * NC + NCF * (wave % NF) + cq;
-    Cols4 cl;
-    if (wave < NF) cl = load_cols4<EK>(e, ncol);
-    const bool more = ct + (int)gridDim.x < tiles;  // uniform over the workgroup
-    if (more) {
-      dma(ct + gridDim.x, (it & 1) ? wb0 : wb1);
-      wait_vmcnt_wlds<NI>();   // everything but the next tile's weights has landed
-    } else {
-      wait_vmcnt_wlds<0>();
+  const int cq = 4 * (grp & (NCF / 4 - 1));   // the lane's first column in the fragment
+  auto ncol_of = [&](int ct) -> int64_t {
+    return SILU ? (cq < H ? (int64_t)ct * H + cq : (int64_t)(e.N / 2) + ct * H + cq - H)
+                : (int64_t)ct * NC + NCF * (wave % NF) + cq;
+  };
+  // One column tile, as in gemm_wlds1p: the explicit vmcnt(0) at the top is the only wait on
+  // vector memory (this tile's weights and epilogue operands, requested a tile earlier), then
+  // the next tile's are requested; operands in two alternating register sets, the
+  // reduction's LDS stores in inline assembly (a use of a loaded register, or an LDS store,
+  // while a direct-to-LDS copy is in flight makes the compiler wait for every request).
+  auto tile = [&](int ct, int8_t* cur, int8_t* nxt, const Cols4& cl, Cols4& cln) {
+    wait_vmcnt_wlds<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    const int ctn = ct + (int)gridDim.x;
+    if (ctn < tiles) {               // uniform over the workgroup
+      dma(ctn, nxt);
+      if (wave < NF) cln = load_cols4<EK>(e, ncol_of(ctn));
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t ncol = ncol_of(ct);
     v4i b[KS][NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -308,7 +313,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       for (int f = 0; f < NF; ++f)
         acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[s][f], a[s], acc[f], 0, 0, 0);
 #pragma unroll
-    for (int f = 0; f < NF; ++f) red[(wave * NF + f) * 64 + lane] = acc[f];
+    for (int f = 0; f < NF; ++f) lds_store_b128(&red[(wave * NF + f) * 64 + lane], acc[f]);
     lds_sync();
     if (wave < NF) {
       v4i sum = red[wave * 64 + lane];
@@ -324,6 +329,19 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       }
     }
     lds_sync();  // the partials of the next tile overwrite the reduction area
+  };
+
+  // the first tile's weights were requested before the row work
+  int ct = blockIdx.x;
+  Cols4 cla, clb;
+  if (ct < tiles && wave < NF) cla = load_cols4<EK>(e, ncol_of(ct));
+  for (;;) {
+    if (ct >= tiles) break;
+    tile(ct, wb0, wb1, cla, clb);
+    ct += gridDim.x;
+    if (ct >= tiles) break;
+    tile(ct, wb1, wb0, clb, cla);
+    ct += gridDim.x;
   }
 }
 
