@@ -130,10 +130,11 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
     return q, s
 
 
-# Largest M that quant_mm takes.  Every column tile quantizes the token rows itself, so the
-# fused launch pays off only for few tokens: measured on MI355X at K = N = 2048 (graph replay,
-# cold weights), one launch vs quant_per_token + w8a8_mm is 4.45 vs 5.31 us at M = 1,
-# 5.19 vs 5.93 at M = 8 and 7.07 vs 6.30 at M = 16.
+# Largest M that quant_mm takes (the kernel's limit: one 16-row block, at most 8 valid rows).
+# Every column tile quantizes the token rows itself, so the fused launch pays off only for few
+# tokens: measured on MI355X (graph replay, cold weights), one launch vs quant_per_token +
+# w8a8_mm is 3.82 vs 4.77 us at M = 1 and 4.14 vs 5.44 at M = 8 for K = N = 2048 (o_proj),
+# 4.98 vs 6.84 at M = 1 and 7.75 vs 7.79 at M = 8 for K = 6144, N = 2048 (down_proj).
 QUANT_MM_MAX_M = 8
 
 
