@@ -188,7 +188,8 @@ WLDSP = [(mt, nc, ks, w) for mt, nc, ks, w in
          [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
           (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
           (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8), (1, 8, 2, 16), (1, 8, 4, 16),
-          (1, 8, 8, 8), (1, 8, 16, 4), (1, 16, 16, 4), (1, 8, 8, 4), (1, 16, 8, 4)]]
+          (1, 8, 8, 8), (1, 8, 16, 4), (1, 16, 16, 4), (1, 8, 8, 4), (1, 16, 8, 4),
+          (1, 8, 6, 16), (2, 8, 6, 16), (1, 8, 12, 8)]]
 
 
 @pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
@@ -209,6 +210,25 @@ def test_persistent_decode_tiles_exact(mt, nc, ks, w, m):
                         (torch.float16, torch.randn(n, device="cuda") * 0.01)):
         out = w8a8_mm(a, wt.t(), sa, sb, dtype, bias, config=config)
         assert np.array_equal(bits(out), oracle_out(a, wt, sa, sb, bias, dtype)), (dtype, bias is None)
+
+
+@pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
+def test_persistent_decode_tiles_one_tile_a_workgroup(mt, nc, ks, w):
+    """The straight single-tile form of the persistent tile (the launcher's choice when the
+    grid covers the column tiles: N = NC x compute units, one row block), exact."""
+    m, k = min(16 * mt, 9), 64 * ks * w
+    n = nc * torch.cuda.get_device_properties(0).multi_processor_count
+    config = Config(16 * mt, nc, 64 * ks, w, 4, 1)
+    say(f"w8a8_mm persistent, one tile a workgroup m={m} k={k} n={n} config={config.name}")
+    a, wt = ints((m, k), 31 + m), ints((n, k), 32)
+    one = torch.ones(1, device="cuda")
+    got = w8a8_mm(a, wt.t(), one, one, raw=True, config=config)
+    assert np.array_equal(np_(got), o.gemm_i32(np_(a), np_(wt)))
+    sa = torch.rand((m, 1), device="cuda") * 1e-2 + 1e-3
+    sb = torch.rand((n, 1), device="cuda") * 1e-2 + 1e-3
+    bias = (torch.randn(n, device="cuda") * 0.01).to(torch.bfloat16)
+    out = w8a8_mm(a, wt.t(), sa, sb, torch.bfloat16, bias, config=config)
+    assert np.array_equal(bits(out), oracle_out(a, wt, sa, sb, bias, torch.bfloat16))
 
 
 # Tiles 384 and 192 columns wide (N a multiple of 192: Llama-3-8B qkv 6144, Qwen3 gate_up
