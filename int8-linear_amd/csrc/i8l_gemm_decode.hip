@@ -1331,7 +1331,7 @@ constexpr WldsPTile kWldsP[] = {{1, 16, 2, 16}, {2, 16, 2, 16}, {1, 32, 2, 16}, 
                                 {4, 16, 2, 16}, {8, 16, 4, 8},  {4, 32, 2, 8},  {1, 8, 2, 16},
                                 {1, 8, 4, 16},  {1, 8, 8, 8},   {1, 8, 16, 4},  {1, 16, 16, 4},
                                 {1, 8, 8, 4},   {1, 16, 8, 4},  {1, 8, 6, 16},  {2, 8, 6, 16},
-                                {1, 8, 12, 8}};
+                                {1, 8, 12, 8},  {1, 8, 4, 8}};
 
 size_t wldsp_lds_bytes(int mt, int nc, int ks, int w) {
   const int nf = nc > 16 ? nc / 16 : 1;
@@ -1410,7 +1410,7 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
   I8L_WLDSP(4, 16, 2, 16) I8L_WLDSP(8, 16, 4, 8) I8L_WLDSP(4, 32, 2, 8) I8L_WLDSP(1, 8, 2, 16)
   I8L_WLDSP(1, 8, 4, 16) I8L_WLDSP(1, 8, 8, 8) I8L_WLDSP(1, 8, 16, 4) I8L_WLDSP(1, 16, 16, 4)
   I8L_WLDSP(1, 8, 8, 4) I8L_WLDSP(1, 16, 8, 4) I8L_WLDSP(1, 8, 6, 16) I8L_WLDSP(2, 8, 6, 16)
-  I8L_WLDSP(1, 8, 12, 8)
+  I8L_WLDSP(1, 8, 12, 8) I8L_WLDSP(1, 8, 4, 8)
 #undef I8L_WLDSP
   return hipErrorInvalidValue;
 }

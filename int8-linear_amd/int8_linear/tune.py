@@ -68,7 +68,7 @@ WLDSP_TILES = [(1, 16, 2, 16), (2, 16, 2, 16), (1, 32, 2, 16), (1, 16, 4, 16),
                (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
                (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8), (1, 8, 2, 16), (1, 8, 4, 16),
                (1, 8, 8, 8), (1, 8, 16, 4), (1, 16, 16, 4), (1, 8, 8, 4), (1, 16, 8, 4),
-               (1, 8, 6, 16), (2, 8, 6, 16), (1, 8, 12, 8)]
+               (1, 8, 6, 16), (2, 8, 6, 16), (1, 8, 12, 8), (1, 8, 4, 8)]
 
 # (MT, NC, KS) of the built weights-through-LDS decode tiles: bm = 16*MT, bn = NC, bk = 64*KS
 WLDS_TILES = [(1, 16, 2), (1, 16, 4), (1, 16, 6), (1, 16, 8), (1, 8, 2), (1, 8, 4), (1, 8, 6),

@@ -189,7 +189,7 @@ WLDSP = [(mt, nc, ks, w) for mt, nc, ks, w in
           (1, 16, 4, 8), (2, 16, 4, 8), (4, 16, 4, 8), (1, 16, 8, 8),
           (4, 16, 2, 16), (8, 16, 4, 8), (4, 32, 2, 8), (1, 8, 2, 16), (1, 8, 4, 16),
           (1, 8, 8, 8), (1, 8, 16, 4), (1, 16, 16, 4), (1, 8, 8, 4), (1, 16, 8, 4),
-          (1, 8, 6, 16), (2, 8, 6, 16), (1, 8, 12, 8)]]
+          (1, 8, 6, 16), (2, 8, 6, 16), (1, 8, 12, 8), (1, 8, 4, 8)]]
 
 
 @pytest.mark.parametrize("mt,nc,ks,w", WLDSP, ids=lambda v: str(v))
