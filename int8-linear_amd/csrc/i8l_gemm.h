@@ -320,8 +320,8 @@ typedef __attribute__((address_space(3))) int8_t lds_i8_t;
 // store: with a direct-to-LDS copy in flight it would first wait for every vector-memory
 // request (it cannot tell that the copy writes elsewhere).  The caller must not store where
 // a copy in flight writes, and waits for the store itself (lgkmcnt, as lds_sync does) before
-// other waves read it.  The s_nops give the 19 wait states an MFMA result needs before a DS
-// instruction may read it (16-pass XDL operations need 18).
+// other waves read it.  The s_nops give 21 wait states (s_nop N waits N + 1): an MFMA result
+// needs up to 18 before a DS instruction may read it (16-pass XDL operations).
 __device__ __forceinline__ void lds_store_b128(void* p, v4i v) {
   const uint32_t a = (uint32_t)(uintptr_t)(lds_i8_t*)p;
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4\n\tds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
