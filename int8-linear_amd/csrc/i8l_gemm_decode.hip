@@ -578,7 +578,8 @@ gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__
 // all of K) once per column tile, as much L2 traffic as the weights themselves at 16 tokens;
 // here A is read once per workgroup.  Each wave reads only its own weight slices, so a
 // buffer is refilled as soon as the wave's own MFMAs have consumed it; the reduction area
-// is shared and is fenced by a barrier on each side.
+// is shared and is fenced by a barrier on each side.  LOOP false: the straight form for a
+// grid with one tile a workgroup (no next tile to request).
 //
 // ACT kActSilu / kActSiluRound: the gate_up projection with the SiLU-and-mul epilogue.  The
 // weight's first N/2 rows are the gate, the last N/2 the up projection; tile t takes gate rows
