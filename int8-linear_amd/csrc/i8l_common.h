@@ -80,6 +80,17 @@ __device__ __forceinline__ float act_to_f32(uint32_t bits, int dtype) {
 }
 
 // ---------------------------------------------------------------- canonical math
+// clamp(rint(v), -128, 127) as the low byte of the result (the byte an int8 code is stored
+// as), without a float-to-int conversion: the clamp is taken first, which gives the same
+// integer since both bounds are integers, and adding 1.5 * 2^23 rounds it to an integer in
+// that one IEEE addition (round half to even, as rint), leaving it in the low mantissa bits
+// of a float whose exponent is fixed: bits = 0x4B400000 + rint(v), two's complement in the
+// low byte for negative codes.
+__device__ __forceinline__ uint32_t code_rne(float v) {
+  const float t = fminf(fmaxf(v, -128.0f), 127.0f) + 12582912.0f;
+  return __float_as_uint(t) & 0xffu;
+}
+
 // exp(x) for float x, defined so that host and device give identical bits: Cody-Waite
 // range reduction x = k*ln2 + r (k = rne(x*log2(e)), ln2 split in a short head and a
 // tail, each subtraction a single fma), then e^r from its Taylor series to degree 7 in

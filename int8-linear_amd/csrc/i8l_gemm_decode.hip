@@ -943,11 +943,7 @@ gemm_wlds1_dq(const uint16_t* __restrict__ X, int64_t ldx, int64_t up,
       for (int q = 0; q < 2; ++q) {
         uint32_t packed = 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          float v = __builtin_rintf(y[p][4 * q + b] * inv);
-          v = fminf(fmaxf(v, -128.0f), 127.0f);
-          packed |= ((uint32_t)(int)v & 0xffu) << (8 * b);
-        }
+        for (int b = 0; b < 4; ++b) packed |= code_rne(y[p][4 * q + b] * inv) << (8 * b);
         word[q] = packed;
       }
       lds_store_b64(abuf + r * S + 8 * cchunk, word[0], word[1]);  // the weight copy is in flight

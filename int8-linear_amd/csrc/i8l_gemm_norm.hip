@@ -257,11 +257,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       for (int h = 0; h < 2; ++h) {
         uint32_t packed = 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          float v = __builtin_rintf(xv[p][4 * h + b] * inv);
-          v = fminf(fmaxf(v, -128.0f), 127.0f);
-          packed |= ((uint32_t)(int)v & 0xffu) << (8 * b);
-        }
+        for (int b = 0; b < 4; ++b) packed |= code_rne(xv[p][4 * h + b] * inv) << (8 * b);
         word[h] = packed;
       }
       lds_store_b64(wb1 + r * S + 8 * cchunk, word[0], word[1]);   // the first tile's copy is in flight

@@ -162,17 +162,6 @@ __device__ __forceinline__ float row_max(float v, const RowPos& p, int nw, float
   return wave_max(p.lane < nw ? sh[p.slot * nw + p.lane] : 0.0f);
 }
 
-// clamp(rint(v), -128, 127) as the low byte of the result (the byte an int8 code is stored
-// as), without a float-to-int conversion: the clamp is taken first, which gives the same
-// integer since both bounds are integers, and adding 1.5 * 2^23 rounds it to an integer in
-// that one IEEE addition (round half to even, as rint), leaving it in the low mantissa bits
-// of a float whose exponent is fixed: bits = 0x4B400000 + rint(v), two's complement in the
-// low byte for negative codes.
-__device__ __forceinline__ uint32_t code_rne(float v) {
-  const float t = fminf(fmaxf(v, -128.0f), 127.0f) + 12582912.0f;
-  return __float_as_uint(t) & 0xffu;
-}
-
 // The quantizer of a row whose values y (J chunks of 8 per lane) are final: absmax over the
 // row, scale and reciprocal, codes stored as 8-byte pieces, the scale by the row's first lane.
 template <int J, bool VEC, bool MULTI, bool FULL = false>

@@ -132,8 +132,8 @@ def quant_per_token(x: torch.Tensor, precise_div: bool = True):
 
 # Largest M that quant_mm takes.  Every column tile quantizes the token rows itself, so the
 # fused launch pays off only for few tokens: measured on MI355X (graph replay, cold weights),
-# one launch vs quant_per_token + w8a8_mm is 3.82 vs 4.77 us at M = 1 and 4.14 vs 5.44 at
-# M = 8 for K = N = 2048 (o_proj), 4.98 vs 6.84 at M = 1 and 7.75 vs 7.79 at M = 8 for
+# one launch vs quant_per_token + w8a8_mm is 3.73 vs 4.77 us at M = 1 and 4.01 vs 5.44 at
+# M = 8 for K = N = 2048 (o_proj), 4.97 vs 6.84 at M = 1 and 7.40 vs 7.79 at M = 8 for
 # K = 6144, N = 2048 (down_proj, whose 12-wave tile takes at most 8 rows).  The K = 2048 tile
 # takes 16-row blocks, but past 8 tokens the fold gains little or loses (5.40 vs 5.54 us at
 # M = 16, 7.03 vs 5.61 at 24, 7.92 vs 5.74 at 32).
