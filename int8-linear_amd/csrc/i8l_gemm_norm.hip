@@ -218,7 +218,7 @@ gemm_wlds1p_nq(const uint16_t* __restrict__ X, const uint16_t* __restrict__ R,
       round_through2<DT>(a, b);
       xv[p][i] = a;
       xv[p][i + 1] = b;
-      am[p] = fmaxf(am[p], fmaxf(fabsf(a), fabsf(b)));
+      am[p] = fmaxf(fmaxf(am[p], fabsf(a)), fabsf(b));   // one max3 with |.| operands
     }
   }
   group_max_n<CH, P>(am);
