@@ -277,9 +277,10 @@ NORM_MM_MAX_M = 8
 # (HIP graph, cold weights, K = 2048), the folded launch takes 3.64 / 4.17 / 4.83 / 4.89 /
 # 6.55 us at N = 4096 and 1 / 2 / 3 / 4 / 8 tokens, against 5.98 / 6.13 / 6.38 / 6.37 / 6.39
 # for add_rmsnorm_quant + w8a8_mm, and 5.96 / 6.16 / 7.19 / 7.51 / 9.21 at N = 12288 against
-# 8.59 / 8.85 / 8.84 / 9.00 / 9.09; in the 28-layer stand-in the folds lose from 5 tokens
-# (27.93 us a layer unfolded at 5 against 28.73 folded, 29.12 against 30.32 at 8).
-NORM_MM_FOLD_M = 4
+# 8.59 / 8.85 / 8.84 / 9.00 / 9.09; in the 28-layer stand-in (SiLU epilogue on) the folds win
+# up to 5 tokens (26.89 us a layer folded at 5 against 27.32 unfolded) and lose from 6 (27.46
+# against 27.18 at 6, 29.22 against 28.44 at 8).
+NORM_MM_FOLD_M = 5
 
 
 def add_rmsnorm_quant_mm(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,

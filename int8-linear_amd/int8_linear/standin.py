@@ -22,7 +22,7 @@ fused_quant.NORM_MM_FOLD_M tokens each add+RMSNorm+quant is folded into the proj
 after it (fused_quant.add_rmsnorm_quant_mm), and from fused_quant.SILU_EPI_MIN_M to
 SILU_EPI_MAX_M tokens gate_up_proj writes silu(gate) * up itself
 (fused_quant.w8a8_mm_silu_mul) for down_proj to quantize; each gives the same bits as the
-kernels it replaces: 4 kernels a layer at 1-4 tokens, 6 at 5-8.
+kernels it replaces: 4 kernels a layer at 1-5 tokens, 6 at 6-8.
 
 Operands follow the reference's stand-in (bench/fuse_quant.py:186-198):
   * x ~ N(0, 1) bf16;
