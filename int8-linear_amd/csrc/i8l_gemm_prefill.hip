@@ -372,7 +372,7 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int S, int BCP = 0>
+template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
          int64_t ldb, Epi e, int K, int group_m) {
@@ -397,8 +397,7 @@ gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B
   staged_tile(blockIdx.x, gridDim.x, num_pid_m, num_pid_n, group_m, pid_m, pid_n);
   const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
   // Global source of each of this lane's J units (token rows past M read row M-1).
@@ -415,13 +414,8 @@ gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B
     const int64_t k0 = (int64_t)min(t, KT - 1) * BK;
     lds_i8* dst = (lds_i8*)(lds + (t % S) * STAGE + wave * 1024);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      if (BCP != 0 && (j * W + wave) * 64 / NCH >= BM)   // weight rows (wave-uniform test)
-        __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0,
-                                         BCP);
-      else
-        __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0, 0);
-    }
+    for (int j = 0; j < J; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0, 0);
   };
 
   v16i acc[FA][FB];
@@ -484,7 +478,7 @@ gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B
 // steps of work before it is needed, and S = 2 is a double buffer.  The last substep's MFMAs
 // then overlap the reads of step t+1's first substep.  The LDS traffic of each substep hides
 // under the matrix work of the one before.
-template <int BM, int BN, int BK, int WM, int WN, int S, int BCP = 0>
+template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
           int64_t ldb, Epi e, int K, int group_m) {
@@ -528,13 +522,8 @@ gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     const int64_t k0 = (int64_t)min(t, KT - 1) * BK;
     lds_i8* dst = (lds_i8*)(lds + (t % S) * STAGE + wave * 1024);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      if (BCP != 0 && (j * W + wave) * 64 / NCH >= BM)   // weight rows (wave-uniform test)
-        __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0,
-                                         BCP);
-      else
-        __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0, 0);
-    }
+    for (int j = 0; j < J; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(gp[j] + k0), dst + j * W * 1024, 16, 0, 0);
   };
 
   v16i acc[FA][FB];
@@ -706,16 +695,11 @@ hipError_t launch_staged_t(const int8_t* a, int64_t lda, const int8_t* b, int64_
 template <int BM, int BN, int BK, int WM, int WN, int S>
 hipError_t launch_dma_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                         const Epi& e, int K, int group_m, hipStream_t st) {
-  // One row tile (M <= BM): each weight byte is read once a call, so its copies carry the
-  // streaming policy, as in the decode kernels; with more row tiles the row tiles of an XCD
-  // re-read the weight panels from its L2.
-  const bool once = e.M <= BM;
-  auto kern = once ? gemm_dma<BM, BN, BK, WM, WN, S, kWeightCpol>
-                   : gemm_dma<BM, BN, BK, WM, WN, S, 0>;
+  auto kern = gemm_dma<BM, BN, BK, WM, WN, S>;
   const size_t shm = std::max<size_t>((size_t)S * (BM + BN) * BK,
                                       tile_epilogue_lds_bytes<BM, BN, WM, WN>());
-  static std::atomic<uint64_t> lds_done[2] = {0, 0};  // devices each form is opted in on
-  lds_opt_in((const void*)kern, shm, lds_done[once]);
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
   return hipGetLastError();
@@ -743,16 +727,11 @@ hipError_t launch_dma(int idx, const i8l_config& c, const int8_t* a, int64_t lda
 template <int BM, int BN, int BK, int WM, int WN, int S>
 hipError_t launch_dmap_t(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                          const Epi& e, int K, int group_m, hipStream_t st) {
-  // One row tile (M <= BM): each weight byte is read once a call, so its copies carry the
-  // streaming policy, as in the decode kernels; with more row tiles the row tiles of an XCD
-  // re-read the weight panels from its L2.
-  const bool once = e.M <= BM;
-  auto kern = once ? gemm_dmap<BM, BN, BK, WM, WN, S, kWeightCpol>
-                   : gemm_dmap<BM, BN, BK, WM, WN, S, 0>;
+  auto kern = gemm_dmap<BM, BN, BK, WM, WN, S>;
   const size_t shm = std::max<size_t>((size_t)S * (BM + BN) * BK,
                                       tile_epilogue_lds_bytes<BM, BN, WM, WN>());
-  static std::atomic<uint64_t> lds_done[2] = {0, 0};  // devices each form is opted in on
-  lds_opt_in((const void*)kern, shm, lds_done[once]);
+  static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
+  lds_opt_in((const void*)kern, shm, lds_done);
   const int tiles = ((e.M + BM - 1) / BM) * (e.N / BN);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), shm, st, a, lda, b, ldb, e, K, group_m);
   return hipGetLastError();
