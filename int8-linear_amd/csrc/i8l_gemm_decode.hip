@@ -1414,6 +1414,8 @@ hipError_t launch_wldsp(const i8l_config& c, const int8_t* a, int64_t lda, const
 
 // The persistent single-step tiles with the SiLU-and-mul epilogue (one 16-row block, 8 or 16
 // columns a tile, bf16 output with no bias or a bf16 bias).
+// Every kWldsP tile of one 16-row block and 8 or 16 columns has its SiLU-epilogue instances
+// in launch_wldsp_silu below (the GPU test of the epilogue walks the same list).
 bool wldsp_silu_ok(const i8l_config& c, int64_t K) {
   return wldsp_ok(c, K) && c.bm == 16 && (c.bn == 8 || c.bn == 16);
 }
@@ -1441,7 +1443,8 @@ hipError_t launch_wldsp_silu(const i8l_config& c, const int8_t* a, int64_t lda, 
   I8L_WLDSP_SILU(16, 2, 16) I8L_WLDSP_SILU(16, 4, 16) I8L_WLDSP_SILU(16, 4, 8)
   I8L_WLDSP_SILU(16, 8, 8) I8L_WLDSP_SILU(8, 2, 16) I8L_WLDSP_SILU(8, 4, 16)
   I8L_WLDSP_SILU(8, 8, 8) I8L_WLDSP_SILU(8, 16, 4) I8L_WLDSP_SILU(16, 16, 4)
-  I8L_WLDSP_SILU(8, 8, 4) I8L_WLDSP_SILU(16, 8, 4)
+  I8L_WLDSP_SILU(8, 8, 4) I8L_WLDSP_SILU(16, 8, 4) I8L_WLDSP_SILU(8, 6, 16)
+  I8L_WLDSP_SILU(8, 12, 8) I8L_WLDSP_SILU(8, 4, 8)
 #undef I8L_WLDSP_SILU
   return hipErrorInvalidValue;
 }

@@ -15,10 +15,17 @@ ACCEPT faster (reference situ_tune.py:237-246).  Kept sets can be merged into th
 table, each entry carrying its stand-in time.  A configuration never changes a result, only
 its speed.
 
+Each linear is tuned in the kernel the stand-in runs for it at that batch (`kernel_of`):
+w8a8_mm ("mm", DecoderStandIn.configs), or for few tokens the norm-folded projection
+("norm", fused_quant.add_rmsnorm_quant_mm, DecoderStandIn.norm_configs: its built tiles) or
+gate_up with the SiLU-and-mul epilogue ("silu", fused_quant.w8a8_mm_silu_mul,
+DecoderStandIn.silu_configs: the built persistent tiles of 8 and 16 columns).  A linear
+whose quantizer is folded in front of it (fused_quant.quant_mm, silu_mul_quant_mm) takes
+that kernel's own tile and is not tuned.  Only "mm" choices become tuned-table rows; the
+folded kernels' choices are reported beside them.
+
 Not done here: the reference's check of its stand-in against two served vLLM runs
-(situ_tune.py:172-211), which needs vLLM and the served models.  o_proj is not tuned when
-the stand-in folds its quantizer into the GEMM (fused_quant.quant_mm, up to
-fused_quant.QUANT_MM_MAX_M tokens), since that kernel takes its own tile.
+(situ_tune.py:172-211), which needs vLLM and the served models.
 
     python -m int8_linear.situ_tune --m 1,8,32,128 [--top 4] [--merge]
 """
@@ -33,10 +40,11 @@ from dataclasses import asdict
 
 import torch
 
+from int8_linear import fused_quant as fq
 from int8_linear import tune
 from int8_linear.kernel import Config, choose_config, default_config, supported, w8a8_mm
 from int8_linear.operands import operands, seed_of
-from int8_linear.standin import SHAPES, DecoderStandIn, per_layer_us
+from int8_linear.standin import HIDDEN, INTER, SHAPES, DecoderStandIn, per_layer_us
 
 ACCEPT = 0.01  # a chosen set must beat the starting one by this fraction to be kept
 
@@ -61,21 +69,86 @@ def isolated_top(m: int, k: int, n: int, top: int, device) -> list[Config]:
     return [c for _, c in sorted(timed, key=lambda t: t[0])[:top]]
 
 
-def step_us(stack: DecoderStandIn, configs: dict, windows: int) -> float:
-    """Microseconds per layer of the stand-in's step under `configs` (a fresh capture)."""
-    stack.configs = dict(configs)
+# (NC, KS, W) of the built norm-folded tiles (bm 16, stages 4), as the library lists them
+NORM_TILES = [(16, 8, 4), (16, 4, 8), (8, 8, 4), (8, 4, 8), (16, 8, 8), (8, 8, 8)]
+
+
+def kernel_of(name: str, fused_norm: bool, fused_silu: bool, fused_down: bool, fused_o: bool,
+              quant_down: bool) -> str | None:
+    """The kernel the stand-in runs for linear `name` under its fold flags (DecoderStandIn.
+    fused_norm, fused_silu, fused_down, fused_o, and whether down_proj takes quant_mm after
+    the SiLU epilogue): "mm", "norm", "silu", or None where a folded quantizer's own tile
+    runs (DecoderStandIn.forward)."""
+    if name == "qkv_proj":
+        return "norm" if fused_norm else "mm"
+    if name == "o_proj":
+        return None if fused_o else "mm"
+    if name == "gate_up_proj":
+        return "norm" if fused_norm else ("silu" if fused_silu else "mm")
+    if fused_silu:
+        return None if quant_down else "mm"
+    return None if fused_down else "mm"
+
+
+def kernels(stack: DecoderStandIn) -> dict:
+    """kernel_of for each linear of the stand-in at its batch size."""
+    quant_down = stack.fused_silu and fq.quant_mm_supported(stack.m, HIDDEN, INTER)
+    return {name: kernel_of(name, stack.fused_norm, stack.fused_silu, stack.fused_down,
+                            stack.fused_o, quant_down) for name in SHAPES}
+
+
+def kind_supported(kind: str, m: int, n: int, k: int, cfg: Config | None) -> bool:
+    """Whether the kernel `kind` takes `cfg` (None: its library default) for this shape."""
+    if kind == "norm":
+        return fq.add_rmsnorm_quant_mm_supported(m, n, k, cfg)
+    if kind == "silu":
+        return fq.w8a8_mm_silu_mul_supported(m, n, k, cfg)
+    return cfg is not None and supported(m, n, k, cfg)
+
+
+def folded_candidates(kind: str, m: int, n: int, k: int) -> list[Config]:
+    """Every built tile of a folded kernel that takes the shape."""
+    if kind == "norm":
+        tiles = [(nc, ks, w) for nc, ks, w in NORM_TILES]
+    else:
+        tiles = [(nc, ks, w) for mt, nc, ks, w in tune.WLDSP_TILES if mt == 1 and nc in (8, 16)]
+    out = []
+    for nc, ks, w in tiles:
+        for g in (1, 2, 4):
+            cfg = Config(16, nc, 64 * ks, w, 4, g)
+            if kind_supported(kind, m, n, k, cfg):
+                out.append(cfg)
+    return out
+
+
+def apply(stack: DecoderStandIn, chosen: dict, kinds: dict) -> None:
+    """Set the stand-in's configurations: each linear's in the dict of the kernel it runs."""
+    stack.configs, stack.norm_configs, stack.silu_configs = {}, {}, {}
+    target = {"mm": stack.configs, "norm": stack.norm_configs, "silu": stack.silu_configs}
+    for name, cfg in chosen.items():
+        if kinds.get(name) in target and cfg is not None:
+            target[kinds[name]][name] = cfg
+
+
+def step_us(stack: DecoderStandIn, configs: dict, windows: int, kinds: dict | None = None
+            ) -> float:
+    """Microseconds per layer of the stand-in's step under `configs` ({linear: Config or
+    None}, each set for the kernel `kinds` names; all w8a8_mm when not given), a fresh
+    capture."""
+    apply(stack, configs, kinds if kinds is not None else dict.fromkeys(configs, "mm"))
     try:
         return per_layer_us(stack, windows)
     finally:
-        stack.configs = {}
+        stack.configs, stack.norm_configs, stack.silu_configs = {}, {}, {}
 
 
-def alternating(stack: DecoderStandIn, options: dict, rounds: int, windows: int) -> dict:
+def alternating(stack: DecoderStandIn, options: dict, rounds: int, windows: int,
+                kinds: dict | None = None) -> dict:
     """Each option timed in fresh captures, in rotation; the median over the rounds."""
     times: dict = {key: [] for key in options}
     for _ in range(rounds):
         for key, configs in options.items():
-            times[key].append(step_us(stack, configs, windows))
+            times[key].append(step_us(stack, configs, windows, kinds))
     return {key: statistics.median(v) for key, v in times.items()}
 
 
@@ -84,44 +157,60 @@ def situ_tune(m: int, layers: int = 28, top: int = 4, rounds: int = 5, windows: 
     """One in-situ pass for batch m.  Returns {"batch", "start", "chosen" (Config dicts),
     "trials", "confirm_us" (start/chosen, when they differ), "kept"}."""
     stack = stack or DecoderStandIn(m, layers=layers, device=device)
-    start = {name: choose_config(m, n, k) for name, (k, n) in SHAPES.items()}
-    tunable = [name for name in SHAPES if not (name == "o_proj" and stack.fused_o)]
+    kinds = kernels(stack)
+    # w8a8_mm linears start from the table's choice, the folded kernels from their default
+    start = {name: choose_config(m, n, k) if kinds[name] == "mm" else None
+             for name, (k, n) in SHAPES.items()}
     current = dict(start)
     trials = []
-    for name in tunable:
+    for name in [name for name in SHAPES if kinds[name] is not None]:
         k, n = SHAPES[name]
-        options = list(dict.fromkeys([current[name], default_config(m, n, k),
-                                      *isolated_top(m, k, n, top, device)]))
+        kind = kinds[name]
+        if kind == "mm":
+            options = [current[name], default_config(m, n, k), *isolated_top(m, k, n, top, device)]
+        else:
+            options = [None, *folded_candidates(kind, m, n, k)]
         best = None
-        for cfg in options:
-            if not supported(m, n, k, cfg):
+        for cfg in dict.fromkeys(options):
+            if not kind_supported(kind, m, n, k, cfg):
                 continue
-            us = step_us(stack, {**current, name: cfg}, windows)
-            trials.append({"layer": name, "config": cfg.name, "us": round(us, 3)})
-            log(f"M={m} {name} {cfg.name}: {us:.2f} us a layer")
+            us = step_us(stack, {**current, name: cfg}, windows, kinds)
+            label = cfg.name if cfg is not None else "default"
+            trials.append({"layer": name, "kernel": kind, "config": label, "us": round(us, 3)})
+            log(f"M={m} {name} ({kind}) {label}: {us:.2f} us a layer")
             if best is None or us < best[1]:
                 best = (cfg, us)
         current[name] = best[0]
-    entry = {"batch": m, "start": {k: asdict(v) for k, v in start.items()},
-             "chosen": {k: asdict(v) for k, v in current.items()}, "trials": trials,
-             "kept": False}
+
+    def dicts(sel):
+        return {k: asdict(v) if v is not None else None for k, v in sel.items()}
+
+    entry = {"batch": m, "kernels": kinds, "start": dicts(start), "chosen": dicts(current),
+             "trials": trials, "kept": False}
     if current != start:
-        t = alternating(stack, {"start": start, "chosen": current}, rounds, windows)
+        t = alternating(stack, {"start": start, "chosen": current}, rounds, windows, kinds)
         entry["confirm_us"] = {key: round(v, 3) for key, v in t.items()}
         entry["kept"] = t["chosen"] < t["start"] * (1 - ACCEPT)
-    log(f"M={m}: " + ", ".join(f"{name} {start[name].name} -> {current[name].name}"
+
+    def label(c):
+        return c.name if c is not None else "default"
+
+    log(f"M={m}: " + ", ".join(f"{name} {label(start[name])} -> {label(current[name])}"
                                for name in SHAPES if start[name] != current[name])
         + f"; confirm {entry.get('confirm_us')}; kept {entry['kept']}")
     return entry
 
 
 def table_rows(entry: dict) -> dict:
-    """A kept entry as tuned-table rows {"KxN": {str(m): {"config", "stand_in_us"}}}."""
+    """A kept entry as tuned-table rows {"KxN": {str(m): {"config", "stand_in_us"}}}: one
+    for each linear that runs w8a8_mm at the batch (the table holds w8a8_mm configurations;
+    an entry without "kernels" has every linear on w8a8_mm)."""
     if not entry["kept"]:
         return {}
+    kinds = entry.get("kernels") or dict.fromkeys(SHAPES, "mm")
     return {f"{k}x{n}": {str(entry["batch"]): {"config": entry["chosen"][name],
                                                 "stand_in_us": entry["confirm_us"]["chosen"]}}
-            for name, (k, n) in SHAPES.items()}
+            for name, (k, n) in SHAPES.items() if kinds.get(name) == "mm"}
 
 
 def main() -> int:

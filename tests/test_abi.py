@@ -358,6 +358,36 @@ def test_situ_tune_writes_only_kept_sets_as_table_rows():
     assert 0 < situ_tune.ACCEPT < 0.05
 
 
+def test_situ_tune_tunes_the_kernel_each_linear_runs():
+    """The in-situ tuner tunes each linear in the kernel the stand-in runs for it: w8a8_mm,
+    the norm-folded projection, gate_up with the SiLU epilogue, or nothing where a folded
+    quantizer's own tile runs (DecoderStandIn.forward); and a kept set writes table rows for
+    its w8a8_mm linears only."""
+    from dataclasses import asdict
+
+    from int8_linear import situ_tune
+    from int8_linear.standin import SHAPES
+
+    def kinds(*flags):
+        return {name: situ_tune.kernel_of(name, *flags) for name in SHAPES}
+
+    # (fused_norm, fused_silu, fused_down, fused_o, quant_down)
+    assert kinds(True, False, True, True, False) == {      # one token
+        "qkv_proj": "norm", "o_proj": None, "gate_up_proj": "norm", "down_proj": None}
+    assert kinds(True, True, False, True, True) == {       # 2-5 tokens
+        "qkv_proj": "norm", "o_proj": None, "gate_up_proj": "norm", "down_proj": None}
+    assert kinds(False, True, False, True, True) == {      # 6-8 tokens
+        "qkv_proj": "mm", "o_proj": None, "gate_up_proj": "silu", "down_proj": None}
+    assert kinds(False, True, False, True, False) == {     # SiLU epilogue, down unfused
+        "qkv_proj": "mm", "o_proj": None, "gate_up_proj": "silu", "down_proj": "mm"}
+    assert set(kinds(False, False, False, False, False).values()) == {"mm"}
+    cfg = asdict(Config(16, 16, 256, 8, 4, 2))
+    entry = {"batch": 8, "kernels": kinds(False, True, False, True, True), "kept": True,
+             "chosen": {name: cfg for name in SHAPES},
+             "confirm_us": {"start": 31.0, "chosen": 30.5}}
+    assert set(situ_tune.table_rows(entry)) == {"2048x4096"}
+
+
 def test_tuner_merge_updates_rows_and_keeps_the_rest(tmp_path):
     """tune.merge writes {"KxN": {M: row}} under the device key, replacing the buckets it is
     given and keeping every other bucket, shape and device (reference merge:

@@ -20,14 +20,15 @@ import torch
 
 from helpers import bits, np_, say
 from int8_linear import fused_quant as fq
+from int8_linear import tune
 from int8_linear.kernel import Config, NotSupported, w8a8_mm
 from oracle import oracle as o
 
 pytestmark = pytest.mark.gpu
 
-# (NC, KS, W) of the persistent single-step tiles with one 16-row block: K = 64 * KS * W
-TILES = [(16, 2, 16), (16, 4, 16), (16, 4, 8), (16, 8, 8), (8, 2, 16), (8, 4, 16), (8, 8, 8),
-         (8, 16, 4), (16, 16, 4), (8, 8, 4), (16, 8, 4)]
+# (NC, KS, W) of every built persistent tile with one 16-row block and 8 or 16 columns (the
+# tiles the SiLU epilogue takes): K = 64 * KS * W
+TILES = [(nc, ks, w) for mt, nc, ks, w in tune.WLDSP_TILES if mt == 1 and nc in (8, 16)]
 
 
 def operands(m, k, n, seed, big_gates=False):
