@@ -679,11 +679,13 @@ extern "C" int i8l_add_rmsnorm_quant_mm(const void* x, const void* residual, con
 // ------------------------------------------------------------------ GEMM + SiLU-and-mul
 // The untuned choice: the persistent single-step tile (one 16-row block) with 16 columns a
 // tile (8 gate and 8 up), 4 waves of 512-byte slices for K = 2048 and two workgroups a
-// compute unit, else the first built form that takes K.
+// compute unit, else the first of these built forms that takes K (K = 6144: 8 columns, 16
+// waves of 384 bytes, as the plain GEMM's tuned entries at that K).
 static bool default_silu_config(int64_t N, int64_t K, i8l_config* c) {
   static const int pref[][4] = {{16, 512, 4, 2}, {16, 256, 8, 2}, {16, 128, 16, 1},
                                 {16, 512, 8, 1}, {16, 256, 16, 1}, {16, 1024, 4, 1},
-                                {8, 512, 4, 2},  {8, 256, 8, 2},   {8, 128, 16, 1}};
+                                {8, 512, 4, 2},  {8, 256, 8, 2},   {8, 128, 16, 1},
+                                {8, 384, 16, 1}, {8, 768, 8, 1}};
   for (const auto& p : pref) {
     const i8l_config t{16, p[0], p[1], p[2], 4, p[3]};
     if (N % t.bn == 0 && wldsp_silu_ok(t, K)) {
