@@ -6,6 +6,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "../../include/int8_linear_amd.h"
@@ -77,6 +78,33 @@ __device__ __forceinline__ void round_through2(float& a, float& b) {
 // Runtime-dtype forms, for code outside the per-element hot loops.
 __device__ __forceinline__ float act_to_f32(uint32_t bits, int dtype) {
   return dtype == I8L_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+// ---------------------------------------------------------------- kernel arguments
+// Kernel arguments into SGPRs, all at once.  The compiler loads each argument where it is
+// first used, and a branch on one (on gridDim, on a size) makes every load after it wait for
+// it: a round trip to the argument segment per branch, each 0.2-0.3 us at a kernel's start
+// (the segment is cold), before the first copy is requested.  Naming the arguments in one
+// empty asm statement issues their loads together, waited for once; later uses read the same
+// registers.  (Each asm statement bounds the scheduling of the loads that feed it, so one
+// statement takes them all.)
+template <typename T>
+__device__ __forceinline__ int64_t pin_value(T v) {
+  if constexpr (std::is_pointer_v<T>)
+    return (int64_t)(uintptr_t)v;
+  else if constexpr (std::is_same_v<T, float>)
+    return __float_as_int(v);                // the bits: no conversion instruction
+  else
+    return (int64_t)v;
+}
+// The grid size and up to 14 arguments.
+template <typename... T>
+__device__ __forceinline__ void pin_vals(T... v) {
+  static_assert(sizeof...(T) <= 14, "at most 14 arguments");
+  const int64_t x[14] = {pin_value(v)...};
+  asm volatile("" ::"s"((int)gridDim.x), "s"((int)gridDim.y), "s"((int)gridDim.z), "s"(x[0]),
+               "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]), "s"(x[6]), "s"(x[7]),
+               "s"(x[8]), "s"(x[9]), "s"(x[10]), "s"(x[11]), "s"(x[12]), "s"(x[13]));
 }
 
 // ---------------------------------------------------------------- canonical math

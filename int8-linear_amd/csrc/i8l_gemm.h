@@ -254,6 +254,21 @@ __device__ __forceinline__ v4i ld16_stream(const int8_t* p) {
   return __builtin_nontemporal_load((const v4i*)p);
 }
 
+// The Epi fields (pin_vals: one round trip for every kernel argument), the grid size and up
+// to 10 more arguments.  blockDim is not read by these kernels: it costs two dependent round
+// trips (the grid size, then a 16-bit load that picks the last workgroup's remainder), so a
+// kernel that needs its wave count takes it as an argument.
+template <typename... T>
+__device__ __forceinline__ void pin_args(const Epi& e, T... more) {
+  static_assert(sizeof...(T) <= 10, "at most 10 more arguments");
+  const int64_t x[10] = {pin_value(more)...};
+  asm volatile("" ::"s"(e.sa), "s"(e.sb), "s"(e.bias), "s"(e.out), "s"(e.ldc), "s"(e.sa_per_row),
+               "s"(e.sb_per_col), "s"(e.bias_dtype), "s"(e.out_dtype), "s"(e.M), "s"(e.N),
+               "s"((int)gridDim.x), "s"((int)gridDim.y), "s"((int)gridDim.z), "s"(x[0]),
+               "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]), "s"(x[6]), "s"(x[7]),
+               "s"(x[8]), "s"(x[9]));
+}
+
 // Column tile of a decode workgroup.  The dispatcher deals workgroups to the 8 XCDs
 // round-robin by linear id; with a multiple of 8 column tiles per row, XCD x is given the
 // contiguous column range [x, x+1) * gridDim.x/8, so the output lines (and the L2 lines

@@ -24,10 +24,11 @@ namespace i8l {
 template <int MT, int NT, int U, int NC>
 __global__ void __launch_bounds__(stream_max_threads(MT, NT))
 gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
-            int64_t ldb, Epi e, int ks) {
+            int64_t ldb, Epi e, int ks, int nw) {
+  pin_args(e, A, lda, B, ldb, ks, nw);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int W = blockDim.x >> 6;
+  const int W = nw;                          // waves (64 * nw threads)
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = xcd_col_tile() * (NC * NT);
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
@@ -204,7 +205,8 @@ __device__ __forceinline__ void wlds_sum_store(const v4i (&acc)[MT][NC < 16 ? 1 
 template <int MT, int NC, int KS, int EK>
 __global__ void __launch_bounds__(wlds_bound(MT, KS, NC))
 gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
-          Epi e, int steps, int nbuf) {
+          Epi e, int steps, int nbuf, int nw) {
+  pin_args(e, A, lda, B, ldb, steps, nbuf, nw);
   constexpr int S = 64 * KS;                 // K bytes per row per step
   constexpr int CPR = S / 16;                // 16-byte chunks per row per step
   // The swizzle XORs a slot with (row & SWM); SWM + 1 is a power of two dividing CPR, so
@@ -226,7 +228,7 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   // wave-uniform values live in scalar registers: the per-lane address work before the first
   // load is then a few 32-bit operations
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int W = blockDim.x >> 6;
+  const int W = nw;                          // waves (64 * nw threads)
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
@@ -351,7 +353,7 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
 template <int MT, int NC, int KS, int EK>
 __global__ void __launch_bounds__(wlds_bound(MT, KS, NC))
 gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
-            int64_t ldb, Epi e, int steps, int nbuf) {
+            int64_t ldb, Epi e, int steps, int nbuf, int nw) {
   constexpr int S = 64 * KS;
   constexpr int CPR = S / 16;
   constexpr int CPR_LOW = CPR & -CPR;
@@ -368,9 +370,10 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   static_assert(NF * NCF == NC, "the tile must be whole column fragments");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
 
+  pin_args(e, A, lda, B, ldb, steps, nbuf, nw);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int W = blockDim.x >> 6;
+  const int W = nw;                          // waves (64 * nw threads)
   const int r16 = lane & 15, grp = lane >> 4;
   const int64_t n0 = xcd_col_tile() * NC;
   const int64_t m0 = (int64_t)blockIdx.y * (16 * MT);
@@ -479,6 +482,7 @@ template <int MT, int NC, int KS, int W, int EK>
 __global__ void __launch_bounds__(64 * W)
 gemm_wlds1(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B, int64_t ldb,
            Epi e) {
+  pin_args(e, A, lda, B, ldb);
   constexpr int S = 64 * KS;
   constexpr int CPR = S / 16;
   constexpr int CPR_LOW = CPR & -CPR;
@@ -1076,11 +1080,14 @@ hipError_t launch_stream_u(const int8_t* a, int64_t lda, const int8_t* b, int64_
   const size_t shm = W > 1 ? (size_t)W * MT * NT * 1024 : 0;
   constexpr int UMAX = stream_unroll(MT, NT);
   if (UMAX == 4 && ks % 4 == 0)
-    hipLaunchKernelGGL((gemm_stream<MT, NT, UMAX, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, UMAX, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks,
+                       W);
   else if (ks % 2 == 0)
-    hipLaunchKernelGGL((gemm_stream<MT, NT, 2, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 2, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks,
+                       W);
   else
-    hipLaunchKernelGGL((gemm_stream<MT, NT, 1, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks);
+    hipLaunchKernelGGL((gemm_stream<MT, NT, 1, NC>), grid, dim3(64 * W), shm, st, a, lda, b, ldb, e, ks,
+                       W);
   return hipGetLastError();
 }
 
@@ -1099,13 +1106,13 @@ hipError_t launch_wlds_steps(const i8l_config& c, const int8_t* a, int64_t lda,
     static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
     lds_opt_in((const void*)kern, kMaxLds, lds_done);
     hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm_a, st, a, lda, b, ldb, e, steps,
-                       steps > 1 ? 2 : 1);
+                       steps > 1 ? 2 : 1, c.warps);
   } else {
     auto kern = gemm_wlds<MT, NC, KS, EK>;
     static std::atomic<uint64_t> lds_done{0};
     lds_opt_in((const void*)kern, kMaxLds, lds_done);
     hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), wlds_lds_bytes(c, kpart), st, a, lda, b,
-                       ldb, e, steps, steps > 1 ? 2 : 1);
+                       ldb, e, steps, steps > 1 ? 2 : 1, c.warps);
   }
   return hipGetLastError();
 }
@@ -1207,6 +1214,7 @@ hipError_t launch_wlds(const i8l_config& c, const int8_t* a, int64_t lda, const 
 template <int Z, int EK, bool XCD>
 __global__ void __launch_bounds__(256)
 splitk_sum(const int32_t* __restrict__ ws, Epi e) {
+  pin_args(e, ws);
   int64_t m, n;
   if constexpr (XCD) {
     const int qpr = e.N >> 5;  // quads a row within one XCD's columns

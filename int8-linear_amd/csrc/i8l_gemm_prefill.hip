@@ -222,6 +222,7 @@ template <int BM, int BN, int BK, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_staged(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
             int64_t ldb, Epi e, int K, int group_m) {
+  pin_args(e, A, lda, B, ldb, K, group_m);
   constexpr int T = 64 * WM * WN;
   constexpr int NCH = BK / 16;
   constexpr int CA = BM * NCH / T;  // 16-byte chunks per thread per stage, activations
@@ -376,6 +377,7 @@ template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dma(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
          int64_t ldb, Epi e, int K, int group_m) {
+  pin_args(e, A, lda, B, ldb, K, group_m);
   constexpr int W = WM * WN;
   constexpr int T = 64 * W;
   constexpr int NCH = BK / 16;
@@ -482,6 +484,7 @@ template <int BM, int BN, int BK, int WM, int WN, int S>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_dmap(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ B,
           int64_t ldb, Epi e, int K, int group_m) {
+  pin_args(e, A, lda, B, ldb, K, group_m);
   constexpr int W = WM * WN;
   constexpr int T = 64 * W;
   constexpr int NCH = BK / 16;

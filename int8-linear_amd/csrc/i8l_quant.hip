@@ -256,6 +256,7 @@ add_rmsnorm_quant_kernel(const uint16_t* __restrict__ x, const uint16_t* __restr
                          const uint16_t* __restrict__ w, float eps, int8_t* __restrict__ q,
                          float* __restrict__ scale, uint16_t* __restrict__ rout, int64_t M,
                          int H, int nw, int rpb, int precise) {
+  pin_vals(x, res, w, eps, q, scale, rout, M, H, nw, rpb, precise);
   static_assert(!FULL || VEC, "FULL rows are vector rows");
   __shared__ double dsh[kMaxWaves];
   __shared__ float fsh[kMaxWaves];
@@ -330,6 +331,7 @@ __global__ void __launch_bounds__(1024)
 silu_mul_quant_kernel(const uint16_t* __restrict__ gu, int8_t* __restrict__ q,
                       float* __restrict__ scale, int64_t M, int I, int nw, int rpb,
                       int precise) {
+  pin_vals(gu, q, scale, M, I, nw, rpb, precise);
   __shared__ float fsh[kMaxWaves];
   const RowPos p = row_pos<MULTI>(nw, rpb);
   if (p.row >= M) return;
@@ -406,6 +408,7 @@ template <int J, int DT, bool VEC, bool MULTI, bool FULL>
 __global__ void __launch_bounds__(1024)
 quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
              float* __restrict__ scale, int64_t M, int H, int nw, int rpb, int precise) {
+  pin_vals(x, ldx, q, scale, M, H, nw, rpb, precise);
   __shared__ float fsh[kMaxWaves];
   const RowPos p = row_pos<MULTI>(nw, rpb);
   if (p.row >= M) return;
