@@ -159,12 +159,13 @@ gemm_stream(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
 // (int32 addition is exact and order-free) through an LDS area that aliases the step ring
 // (every wave's last fragment reads of the ring are done at the first barrier, and no DMA
 // is outstanding after the last step's wait), then the epilogue; fragment fr = i * NF + f is
-// stored by wave fr % W, which loaded its epilogue operands (cl0, sa0) early when fr == wave.
-template <int MT, int NC, int EK>
+// stored by wave fr % W, which loaded the epilogue operands of its first KP fragments (fr =
+// wave + j * W, j < KP: clp[j], sap[j]) before its main loop.
+template <int MT, int NC, int EK, int KP>
 __device__ __forceinline__ void wlds_sum_store(const v4i (&acc)[MT][NC < 16 ? 1 : NC / 16],
                                                int8_t* lds, const Epi& e, int W, int wave,
                                                int lane, int64_t m0, int64_t n0,
-                                               const Cols4& cl0, float sa0) {
+                                               const Cols4 (&clp)[KP], const float (&sap)[KP]) {
   constexpr int NCF = NC < 16 ? NC : 16;
   constexpr int NF = NC / NCF;
   constexpr int FR = MT * NF;
@@ -178,7 +179,10 @@ __device__ __forceinline__ void wlds_sum_store(const v4i (&acc)[MT][NC < 16 ? 1 
       for (int f = 0; f < NF; ++f) red[(wave * FR + q * NF + f) * 64 + lane] = acc[q][f];
     __syncthreads();
   }
-  for (int fr = wave; fr < FR; fr += W) {
+#pragma unroll
+  for (int j = 0; j < FR; ++j) {
+    const int fr = wave + j * W;
+    if (fr >= FR) break;
     v4i sum;
     if (W > 1) {
       sum = red[fr * 64 + lane];
@@ -194,8 +198,8 @@ __device__ __forceinline__ void wlds_sum_store(const v4i (&acc)[MT][NC < 16 ? 1 
     const int64_t m = m0 + 16 * (fr / NF) + r16;
     const int64_t n = n0 + NCF * (fr % NF) + 4 * grp;
     if (m < e.M && 4 * grp < NCF) {
-      if (fr == wave)
-        store4s<EK>(e, m, n, sum, cl0, sa0);
+      if (j < KP)
+        store4s<EK>(e, m, n, sum, clp[j < KP ? j : 0], sap[j < KP ? j : 0]);
       else
         store4<EK>(e, m, n, sum);
     }
@@ -308,14 +312,22 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
   };
 
   issue(a0, 0, steps > 1);
-  // The wave that stores fragment fr (fr % W == wave) loads its epilogue operands now,
-  // behind the first step, so their latency hides under the main loop.
-  Cols4 cl0;
-  float sa0 = 0.0f;
-  if (wave < FR && 4 * grp < NCF) {
-    const int64_t m = m0 + 16 * (wave / NF) + r16;
-    cl0 = load_cols4<EK>(e, n0 + NCF * (wave % NF) + 4 * grp);
-    sa0 = load_sa<EK>(e, m < e.M ? m : 0);
+  // The wave that stores fragment fr (fr % W == wave) loads the epilogue operands of its
+  // first KP fragments now, behind the first step, so their latency hides under the main
+  // loop (a fragment past them would load its operands after the cross-wave sum: a round
+  // trip of ~0.5 us in the 64x32 tile of 4 waves, two fragments a wave).
+  constexpr int KP = 1;                      // (more would spill in the register-bound tiles)
+  Cols4 clp[KP];
+  float sap[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    sap[j] = 0.0f;
+    const int fr = wave + j * W;
+    if (fr < FR && 4 * grp < NCF) {
+      const int64_t m = m0 + 16 * (fr / NF) + r16;
+      clp[j] = load_cols4<EK>(e, n0 + NCF * (fr % NF) + 4 * grp);
+      sap[j] = load_sa<EK>(e, m < e.M ? m : 0);
+    }
   }
   // Steady state: every step's loads are issued before the wait for the previous step, and
   // the wait leaves exactly one step's loads outstanding.  The LDS reads of a step complete
@@ -340,7 +352,7 @@ gemm_wlds(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ 
     compute(a0, i);
   }
 
-  wlds_sum_store<MT, NC, EK>(acc, lds, e, W, wave, lane, m0, n0, cl0, sa0);
+  wlds_sum_store<MT, NC, EK, KP>(acc, lds, e, W, wave, lane, m0, n0, clp, sap);
 }
 
 // gemm_wlds with the activations copied through LDS too: a wave's step buffer holds its NC
@@ -453,12 +465,18 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   };
 
   issue(0, steps > 1);
-  Cols4 cl0;
-  float sa0 = 0.0f;
-  if (wave < FR && 4 * grp < NCF) {
-    const int64_t m = m0 + 16 * (wave / NF) + r16;
-    cl0 = load_cols4<EK>(e, n0 + NCF * (wave % NF) + 4 * grp);
-    sa0 = load_sa<EK>(e, m < e.M ? m : 0);
+  constexpr int KP = FR < 4 ? FR : 4;        // fragments a wave stores with operands loaded now
+  Cols4 clp[KP];
+  float sap[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    sap[j] = 0.0f;
+    const int fr = wave + j * W;
+    if (fr < FR && 4 * grp < NCF) {
+      const int64_t m = m0 + 16 * (fr / NF) + r16;
+      clp[j] = load_cols4<EK>(e, n0 + NCF * (fr % NF) + 4 * grp);
+      sap[j] = load_sa<EK>(e, m < e.M ? m : 0);
+    }
   }
   // each step's copy is requested before the wait for the one before, which leaves exactly
   // one step's DMA outstanding (the epilogue operands were requested between steps 0 and 1,
@@ -471,7 +489,7 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   }
   wait_vmcnt_wlds<0>();
   compute(i);
-  wlds_sum_store<MT, NC, EK>(acc, lds, e, W, wave, lane, m0, n0, cl0, sa0);
+  wlds_sum_store<MT, NC, EK, KP>(acc, lds, e, W, wave, lane, m0, n0, clp, sap);
 }
 
 // The same tile when every wave's K slice is a single step (K == W * 64 * KS), with the
