@@ -480,12 +480,30 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   }
   // each step's copy is requested before the wait for the one before, which leaves exactly
   // one step's DMA outstanding (the epilogue operands were requested between steps 0 and 1,
-  // so they have landed too)
+  // so they have landed too); with three buffers, two steps ahead: the wait for step i
+  // leaves steps i+1 and i+2 in flight (a step of a CU's four waves takes ~0.5 us to land,
+  // longer than its MFMAs)
   int i = 0;
-  for (; i + 1 < steps; ++i) {
-    issue(i + 1, true);
-    wait_vmcnt_wlds<NI>();
-    compute(i);
+  bool deep = false;
+  if constexpr (2 * NI < 64) deep = nbuf >= 3 && steps > 2;
+  if (deep) {
+    if constexpr (2 * NI < 64) {
+      issue(1, true);
+      for (; i + 2 < steps; ++i) {
+        issue(i + 2, true);
+        wait_vmcnt_wlds<2 * NI>();
+        compute(i);
+      }
+      wait_vmcnt_wlds<NI>();
+      compute(i);
+      ++i;
+    }
+  } else {
+    for (; i + 1 < steps; ++i) {
+      issue(i + 1, true);
+      wait_vmcnt_wlds<NI>();
+      compute(i);
+    }
   }
   wait_vmcnt_wlds<0>();
   compute(i);
@@ -1060,13 +1078,20 @@ size_t wlds_lds_bytes(const i8l_config& c, int64_t K) {
 
 // LDS of gemm_wlds_a: the step ring of weight and activation rows, or the reduction area
 // that aliases it, whichever is larger.
-size_t wlds_a_lds_bytes(const i8l_config& c, int64_t K) {
-  const int64_t steps = K / ((int64_t)c.bk * c.warps);
-  const int nbuf = steps > 1 ? 2 : 1;
+size_t wlds_a_lds_bytes(const i8l_config& c, int64_t K, int nbuf) {
   const int nf = c.bn > 16 ? c.bn / 16 : 1;
   const size_t ring = (size_t)c.warps * nbuf * (c.bn + c.bm) * c.bk;
   const size_t red = (size_t)c.warps * (c.bm / 16) * nf * 1024;
   return std::max(ring, red);
+}
+
+// Buffers of gemm_wlds_a's ring: three (two steps in flight) for a stages-3 config with
+// group_m 3 (wlds_ok takes it only where K has more than two steps a wave and the three
+// buffers fit the LDS), else two (one step a wave: one).
+int wlds_a_nbuf(const i8l_config& c, int64_t K) {
+  const int64_t steps = K / ((int64_t)c.bk * c.warps);
+  if (c.stages == 3 && c.group_m == 3 && steps > 2) return 3;
+  return steps > 1 ? 2 : 1;
 }
 
 // LDS of gemm_wlds1 (one step a wave): its weight buffers and, after them, the reduction area.
@@ -1087,6 +1112,8 @@ bool wlds_ok(const i8l_config& c, int64_t K) {
   const bool one_step = K == (int64_t)c.bk * c.warps &&
                         wlds1_built(c.bm / 16, c.bn, c.warps, c.bk / 64);
   if (!one_step && !wlds_multi_fits(c.bm / 16, c.bn, c.bk / 64)) return false;
+  if (c.group_m == 3)   // the three-buffer ring of gemm_wlds_a: more than two steps a wave
+    return K > 2 * (int64_t)c.bk * c.warps && wlds_a_lds_bytes(c, K, 3) <= kMaxLds;
   return (one_step ? wlds1_lds_bytes(c.bm / 16, c.bn, c.bk / 64, c.warps)
                    : wlds_lds_bytes(c, K)) <= kMaxLds;
 }
@@ -1118,13 +1145,14 @@ hipError_t launch_wlds_steps(const i8l_config& c, const int8_t* a, int64_t lda,
                              int parts, hipStream_t st) {
   const int steps = (int)(kpart / ((int64_t)c.bk * c.warps));
   const dim3 grid(e.N / NC, (e.M + 16 * MT - 1) / (16 * MT), parts);
-  const size_t shm_a = wlds_a_lds_bytes(c, kpart);
+  const int nbuf_a = wlds_a_nbuf(c, kpart);
+  const size_t shm_a = wlds_a_lds_bytes(c, kpart, nbuf_a);
   if (shm_a <= kMaxLds) {
     auto kern = gemm_wlds_a<MT, NC, KS, EK>;
     static std::atomic<uint64_t> lds_done{0};  // devices this kernel is opted in on
     lds_opt_in((const void*)kern, kMaxLds, lds_done);
     hipLaunchKernelGGL(kern, grid, dim3(64 * c.warps), shm_a, st, a, lda, b, ldb, e, steps,
-                       steps > 1 ? 2 : 1, c.warps);
+                       nbuf_a, c.warps);
   } else {
     auto kern = gemm_wlds<MT, NC, KS, EK>;
     static std::atomic<uint64_t> lds_done{0};

@@ -99,9 +99,10 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
             if mt > need:
                 continue  # one row block covering M, or several smaller ones
             for w in (4, 8, 12, 16):
-                cfg = Config(16 * mt, nc, 64 * ks, w, 3, 1)
-                if supported(m, n, k, cfg):
-                    out.append(cfg)
+                for g in (1, 3):             # group_m 3: the three-buffer ring
+                    cfg = Config(16 * mt, nc, 64 * ks, w, 3, g)
+                    if supported(m, n, k, cfg):
+                        out.append(cfg)
         for mt, nc, ks, w in WLDSP_TILES:
             if mt > need:
                 continue

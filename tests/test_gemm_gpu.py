@@ -266,12 +266,15 @@ WLDS = [(mt, nc, ks) for mt, nc, ks in
 
 
 @pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
-@pytest.mark.parametrize("steps", [1, 2, 3, 4])
+@pytest.mark.parametrize("steps", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("waves", [4, 8, 12, 16])
-def test_weights_through_lds_schedule(tile, steps, waves):
+@pytest.mark.parametrize("ring", [1, 3], ids=["two_buffers", "three_buffers"])
+def test_weights_through_lds_schedule(tile, steps, waves, ring):
+    """group_m 3: the three-buffer ring of the activations-through-LDS tile (more than two
+    steps a wave), whose loop and tail differ from the two-buffer one's."""
     mt, nc, ks = tile
     k, n = 64 * ks * waves * steps, 512
-    cfg = Config(16 * mt, nc, 64 * ks, waves, 3, 1)
+    cfg = Config(16 * mt, nc, 64 * ks, waves, 3, ring)
     if not kernel.supported(16 * mt, n, k, cfg):
         pytest.skip(f"{cfg.name} is not built for K={k}")
     for m in {1: (1, 5, 16), 2: (17, 32), 4: (33, 64), 8: (65, 100, 128)}[mt]:
