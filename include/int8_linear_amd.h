@@ -55,7 +55,9 @@ enum {
  *                staged through registers, 3..8 a ring of that many direct-to-LDS buffers,
  *                >= 10 a ring of stages - 8 buffers (2: a double buffer) with fragment reads
  *                overlapped with the MFMAs (prefill)
- *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); with
+ *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); stages 3
+ *                with bn <= 64: 3 keeps two K steps in flight (three step buffers a
+ *                wave), else one; with
  *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4); with
  *                stages 5, the parts K is split into (2, 4 or 8)
  * A config the library was not built for returns I8L_UNSUPPORTED.
