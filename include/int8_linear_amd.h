@@ -57,8 +57,7 @@ enum {
  *                overlapped with the MFMAs (prefill)
  *   group_m    : rows of tiles walked together for L2 reuse (1 = row-major order); stages 3
  *                with bn <= 64: 3 keeps two K steps in flight (three step buffers a
- *                wave), else one; with
- *                stages 4, the workgroups a compute unit runs at once (1, 2 or 4); with
+ *                wave), 4 three (four buffers), else one; with stages 4, the workgroups a compute unit runs at once (1, 2 or 4); with
  *                stages 5, the parts K is split into (2, 4 or 8)
  * A config the library was not built for returns I8L_UNSUPPORTED.
  */

@@ -482,11 +482,31 @@ gemm_wlds_a(const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict_
   // one step's DMA outstanding (the epilogue operands were requested between steps 0 and 1,
   // so they have landed too); with three buffers, two steps ahead: the wait for step i
   // leaves steps i+1 and i+2 in flight (a step of a CU's four waves takes ~0.5 us to land,
-  // longer than its MFMAs)
+  // longer than its MFMAs); with four, three steps ahead.  A depth whose outstanding DMA
+  // would not fit the vmcnt counter falls back to the next smaller one.
   int i = 0;
-  bool deep = false;
-  if constexpr (2 * NI < 64) deep = nbuf >= 3 && steps > 2;
-  if (deep) {
+  int depth = 1;
+  if constexpr (2 * NI < 64)
+    if (nbuf >= 3 && steps > 2) depth = 2;
+  if constexpr (3 * NI < 64)
+    if (nbuf >= 4 && steps > 3) depth = 3;
+  if (depth == 3) {
+    if constexpr (3 * NI < 64) {
+      issue(1, true);
+      issue(2, true);
+      for (; i + 3 < steps; ++i) {
+        issue(i + 3, true);
+        wait_vmcnt_wlds<3 * NI>();
+        compute(i);
+      }
+      wait_vmcnt_wlds<2 * NI>();
+      compute(i);
+      ++i;
+      wait_vmcnt_wlds<NI>();
+      compute(i);
+      ++i;
+    }
+  } else if (depth == 2) {
     if constexpr (2 * NI < 64) {
       issue(1, true);
       for (; i + 2 < steps; ++i) {
@@ -1085,12 +1105,13 @@ size_t wlds_a_lds_bytes(const i8l_config& c, int64_t K, int nbuf) {
   return std::max(ring, red);
 }
 
-// Buffers of gemm_wlds_a's ring: three (two steps in flight) for a stages-3 config with
-// group_m 3 (wlds_ok takes it only where K has more than two steps a wave and the three
-// buffers fit the LDS), else two (one step a wave: one).
+// Buffers of gemm_wlds_a's ring: group_m for a stages-3 config with group_m 3 or 4
+// (group_m - 1 steps in flight; wlds_ok takes it only where K has more than that many
+// steps a wave and the buffers fit the LDS), else two (one step a wave: one).
 int wlds_a_nbuf(const i8l_config& c, int64_t K) {
   const int64_t steps = K / ((int64_t)c.bk * c.warps);
-  if (c.stages == 3 && c.group_m == 3 && steps > 2) return 3;
+  if (c.stages == 3 && (c.group_m == 3 || c.group_m == 4) && steps > c.group_m - 1)
+    return c.group_m;
   return steps > 1 ? 2 : 1;
 }
 
@@ -1112,8 +1133,11 @@ bool wlds_ok(const i8l_config& c, int64_t K) {
   const bool one_step = K == (int64_t)c.bk * c.warps &&
                         wlds1_built(c.bm / 16, c.bn, c.warps, c.bk / 64);
   if (!one_step && !wlds_multi_fits(c.bm / 16, c.bn, c.bk / 64)) return false;
-  if (c.group_m == 3)   // the three-buffer ring of gemm_wlds_a: more than two steps a wave
-    return K > 2 * (int64_t)c.bk * c.warps && wlds_a_lds_bytes(c, K, 3) <= kMaxLds;
+  if (c.group_m == 3 || c.group_m == 4) {   // gemm_wlds_a's deeper rings
+    const int ni = (c.bn + c.bm) * c.bk / 1024;   // DMA instructions a wave a step
+    return K > (int64_t)(c.group_m - 1) * c.bk * c.warps && (c.group_m - 1) * ni < 64 &&
+           wlds_a_lds_bytes(c, K, c.group_m) <= kMaxLds;
+  }
   return (one_step ? wlds1_lds_bytes(c.bm / 16, c.bn, c.bk / 64, c.warps)
                    : wlds_lds_bytes(c, K)) <= kMaxLds;
 }

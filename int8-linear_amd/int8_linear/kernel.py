@@ -42,7 +42,7 @@ class Config:
       stages == 3: weights copied through LDS with direct-to-LDS loads; each of the
         `warps` waves owns one K slice taken bk bytes per step (K a multiple of bk * warps);
         group_m == 3 keeps two steps in flight (three step buffers a wave; more than two
-        steps a wave), else one.
+        steps a wave), group_m == 4 three (four buffers; more than three steps), else one.
       stages == 4: the same with one K step a wave (K == bk * warps), each workgroup walking
         several column tiles with its activations held in registers.
       stages == 5: the stages-3 tile (up to 64 columns) with K split into group_m (2, 4 or 8)

@@ -99,7 +99,7 @@ def candidate_configs(m: int, k: int, n: int) -> list[Config]:
             if mt > need:
                 continue  # one row block covering M, or several smaller ones
             for w in (4, 8, 12, 16):
-                for g in (1, 3):             # group_m 3: the three-buffer ring
+                for g in (1, 3, 4):          # group_m 3 / 4: the three- / four-buffer ring
                     cfg = Config(16 * mt, nc, 64 * ks, w, 3, g)
                     if supported(m, n, k, cfg):
                         out.append(cfg)

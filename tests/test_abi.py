@@ -112,6 +112,22 @@ def test_every_tuner_candidate_tile_is_built():
                    for w in (4, 8, 16) for steps in (1, 2)), (mt, nc, ks)
 
 
+def test_deeper_rings_take_only_what_they_can_keep_in_flight():
+    """group_m 3 / 4 of the stages-3 tile keep two / three K steps in flight: each needs more
+    steps a wave than that, its buffers within the LDS, and its outstanding copies (steps in
+    flight x the step's 1 KiB copy instructions) below the 64 the vmcnt counter holds."""
+    n = 4096
+    for g, need in ((3, 3), (4, 4)):
+        cfg = Config(16, 64, 128, 4, 3, g)      # 80 rows x 128 bytes: 10 copies a step
+        for steps in range(1, 7):
+            assert kernel.supported(16, n, steps * 4 * 128, cfg) == (steps >= need), (g, steps)
+    # 96 rows x 256 bytes: 24 copies a step, so two steps (48) fit the counter, three (72) not
+    cfg3, cfg4 = Config(32, 64, 256, 1, 3, 3), Config(32, 64, 256, 1, 3, 4)
+    assert kernel.supported(32, n, 5 * 256, cfg3) and not kernel.supported(32, n, 5 * 256, cfg4)
+    # four buffers of 32 rows x 512 bytes a wave over 4 waves: 256 KiB, beyond the LDS
+    assert not kernel.supported(1, n, 5 * 4 * 512, Config(16, 16, 512, 4, 3, 4))
+
+
 def test_supported_decline_rule_matches_reference():
     # kernel.py:228-229 of the reference: N % bn or K % bk declines
     assert not kernel.supported(4, 64, 100)

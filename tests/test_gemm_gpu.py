@@ -268,10 +268,10 @@ WLDS = [(mt, nc, ks) for mt, nc, ks in
 @pytest.mark.parametrize("tile", WLDS, ids=lambda t: f"mt{t[0]}_nc{t[1]}_ks{t[2]}")
 @pytest.mark.parametrize("steps", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("waves", [4, 8, 12, 16])
-@pytest.mark.parametrize("ring", [1, 3], ids=["two_buffers", "three_buffers"])
+@pytest.mark.parametrize("ring", [1, 3, 4], ids=["two_buffers", "three_buffers", "four_buffers"])
 def test_weights_through_lds_schedule(tile, steps, waves, ring):
-    """group_m 3: the three-buffer ring of the activations-through-LDS tile (more than two
-    steps a wave), whose loop and tail differ from the two-buffer one's."""
+    """group_m 3 / 4: the three- / four-buffer ring of the activations-through-LDS tile (more
+    than two / three steps a wave), whose loops and tails differ from the two-buffer one's."""
     mt, nc, ks = tile
     k, n = 64 * ks * waves * steps, 512
     cfg = Config(16 * mt, nc, 64 * ks, waves, 3, ring)
